@@ -1,0 +1,61 @@
+// Top-k weighted unpermute-combine (deterministic, no atomics).
+//
+// y[t] = bf16( sum_s w[t,s] * out[inv[t,s]]  +  gate[t] * out[sh_row0 + t] )
+// The routed sum is the weighted slot sum of the reference (qwen3_5.py:871-872, dense path;
+// the sparse path's index_add_, :838-839, adds the same terms), the second term is the gated
+// shared expert (qwen3_5.py:903-904). Accumulation is fp32 in slot order 0..k-1, then the
+// shared term, with one rounding to bf16 at the end. Pairs with inv < 0 (expert id out of
+// range) contribute nothing.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace lbmoe {
+
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
+                                                      const int32_t* __restrict__ inv,
+                                                      const uint16_t* __restrict__ topw,
+                                                      const float* __restrict__ sgate, int T,
+                                                      int k, int H, int sh_row0,
+                                                      uint16_t* __restrict__ y) {
+  const int t = blockIdx.x;
+  for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; ++s) {
+      const int64_t ts = static_cast<int64_t>(t) * k + s;
+      const int p = inv[ts];
+      if (p < 0) continue;
+      const float w = bf2f(topw[ts]);
+      const u32x4 o = ld16(rows + static_cast<int64_t>(p) * H + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += w * bf_lo(o[i]);
+        acc[2 * i + 1] += w * bf_hi(o[i]);
+      }
+    }
+    if (sgate != nullptr) {
+      const float g = sgate[t];
+      const u32x4 o = ld16(rows + static_cast<int64_t>(sh_row0 + t) * H + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += g * bf_lo(o[i]);
+        acc[2 * i + 1] += g * bf_hi(o[i]);
+      }
+    }
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk[i] = pack_bf2(acc[2 * i], acc[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + c) = pk;
+  }
+}
+
+hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
+                          const float* sgate, int64_t T, int k, int H, bool shared, void* y,
+                          hipStream_t s) {
+  combine_kernel<<<static_cast<unsigned>(T), 256, 0, s>>>(
+      static_cast<const uint16_t*>(out_rows), inv, static_cast<const uint16_t*>(topw),
+      shared ? sgate : nullptr, static_cast<int>(T), k, H, static_cast<int>(T) * k,
+      static_cast<uint16_t*>(y));
+  return hipGetLastError();
+}
+
+}  // namespace lbmoe

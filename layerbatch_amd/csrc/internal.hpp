@@ -1,0 +1,89 @@
+// Host-side internals of liblbmoe: workspace layout and kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/lbmoe.h"
+
+namespace lbmoe {
+
+// Entries of the permutation handled by one block of the count/scatter kernels.
+constexpr int kPermChunk = 1024;
+
+inline int64_t perm_blocks(int64_t V) { return (V + kPermChunk - 1) / kPermChunk; }
+
+enum Region {
+  R_LOGITS = 0, R_IDX, R_TOPW, R_SGATE, R_COUNTS, R_OFFSETS, R_PERM_TOK, R_PERM_SLOT, R_INV,
+  R_ACT, R_OUT,
+  // private regions (not exposed through lbmoe_workspace_region)
+  R_HIST, R_BASE, R_LRANK, R_XQ, R_XS, R_ACTQ, R_ACTS,
+  R_COUNT_
+};
+constexpr int kPublicRegions = R_OUT + 1;
+
+struct WsLayout {
+  size_t off[R_COUNT_];
+  size_t bytes[R_COUNT_];
+  size_t total;
+};
+
+WsLayout ws_layout(const lbmoe_layer& L, int64_t T);
+// Layout of the permutation scratch (hist, base, lrank) alone.
+void perm_scratch_layout(int64_t T, int k, int E, size_t* hist_off, size_t* base_off,
+                         size_t* lrank_off, size_t* total);
+
+// Per-group view of the expert weights for kernels. Groups 0..E-1 are the routed experts
+// (rows offsets[g] .. offsets[g]+counts[g]-1 of the permuted arrays); group E is the shared
+// expert, which takes all T tokens in order at rows sh_row0 .. sh_row0+T-1. A launch covers
+// groups g0 .. g0+groups-1.
+struct GroupWeights {
+  const void* gate_up;      // [E,2I,H]
+  const void* down;         // [E,H,I]
+  const float* gate_up_scale;
+  const float* down_scale;
+  const void* sh_gate;      // [Is,H]
+  const void* sh_up;        // [Is,H]
+  const void* sh_down;      // [H,Is]
+  const float* sh_gate_scale;
+  const float* sh_up_scale;
+  const float* sh_down_scale;
+  int E, H, I, Is;
+  int g0, groups;
+  int sh_row0;
+};
+
+// ---- launchers (each returns hipError_t of the launch) ----------------------------------
+hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
+                                void* logits, hipStream_t s);
+hipError_t launch_route_topk(const void* logits, const float* bias, const void* x,
+                             const void* w_sg, int64_t T, int E, int H, int k, void* idx,
+                             int idx_bytes, void* topw, float* sgate, hipStream_t s);
+hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int E,
+                          bool shared_rows, int32_t* counts, int32_t* offsets,
+                          int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,
+                          int32_t* hist, int32_t* base, int32_t* lrank, hipStream_t s);
+hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
+                               const int32_t* offsets, const int32_t* perm_tok, int64_t T,
+                               int act_ld, void* act, hipStream_t s);
+hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
+                            const int32_t* counts, const int32_t* offsets, int64_t T,
+                            void* out, hipStream_t s);
+hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
+                          const float* sgate, int64_t T, int k, int H, bool shared,
+                          void* y, hipStream_t s);
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
+hipError_t launch_quant_blocks_fp8(const void* w, int64_t batch, int N, int K, void* q,
+                                   float* scale, hipStream_t s);
+hipError_t launch_quant_groups_fp8(const void* a, int64_t rows, int cols, int ld, void* q,
+                                   float* scale, hipStream_t s);
+hipError_t launch_gate_up_fp8(const GroupWeights& gw, const void* xq, const float* xs,
+                              const int32_t* counts, const int32_t* offsets,
+                              const int32_t* perm_tok, int64_t T, int act_ld, void* act,
+                              hipStream_t s);
+hipError_t launch_down_fp8(const GroupWeights& gw, const void* actq, const float* acts,
+                           int act_ld, const int32_t* counts, const int32_t* offsets,
+                           int64_t T, void* out, hipStream_t s);
+
+}  // namespace lbmoe

@@ -1,0 +1,261 @@
+// Expert sort of the (token, slot) routing pairs.
+//
+// Restates the ordering of the reference's _forward_sparse (nanovllm/models/qwen3_5.py:823-833):
+// experts ascending, and within an expert torch.where over the [k, T] mask, i.e. (slot, token)
+// row-major. Entries are visited in slot-major order v = s*T + t, so a stable counting sort
+// on the expert id yields exactly the key (expert, slot, token).
+//
+// Three passes, integer-only and deterministic:
+//   count   one wave per chunk of kPermChunk entries: stable rank of every entry among the
+//           chunk's entries of the same expert (64-lane ballot matching on the expert bits),
+//           per-chunk histogram hist[e][chunk].
+//   scan    one workgroup: exclusive scan of hist in (expert, chunk) order -> base[e][chunk],
+//           counts[e], offsets[e].
+//   scatter one wave per chunk: pos = base[e][chunk] + rank -> perm_tok, perm_slot, inv.
+// When all entries fit one chunk the three passes run in a single one-wave kernel.
+// Entries whose expert id lies outside [0, E) are left out of every list and get inv = -1.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace lbmoe {
+
+template <int IB>
+__device__ __forceinline__ int load_expert(const void* idx, int64_t i) {
+  if constexpr (IB == 8) return static_cast<int>(reinterpret_cast<const int64_t*>(idx)[i]);
+  else return reinterpret_cast<const int32_t*>(idx)[i];
+}
+
+// Stable in-wave match: lanes with equal expert id (among `m`) get consecutive ranks.
+__device__ __forceinline__ uint64_t match_expert(int e, uint64_t m, int nbits) {
+  for (int b = 0; b < nbits; ++b) {
+    const bool on = (e >> b) & 1;
+    const uint64_t bal = __ballot(on);
+    m &= on ? bal : ~bal;
+  }
+  return m;
+}
+
+// Ranks one chunk's entries. Returns per-lane (expert, rank) for round r in e_out/rk_out.
+template <int IB, int ROUNDS>
+__device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E, int nbits,
+                                           int V, int v0, int* run, int (&e_out)[ROUNDS],
+                                           int (&rk_out)[ROUNDS]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int r = 0; r < ROUNDS; ++r) {
+    const int v = v0 + r * kWave + lane;
+    int e = -1;
+    if (v < V) {
+      const int s = v / T;
+      const int t = v - s * T;
+      e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
+    }
+    const bool valid = (e >= 0) && (e < E);
+    const uint64_t m = match_expert(valid ? e : 0, __ballot(valid), nbits);
+    int rank = -1;
+    if (valid) {
+      const int before = run[e];                       // same address for the whole group
+      rank = before + mask_rank(m);
+      if (mask_rank(m) == 0) run[e] = before + __popcll(m);   // group leader
+    }
+    e_out[r] = valid ? e : -1;
+    rk_out[r] = rank;
+  }
+}
+
+constexpr int kRounds = kPermChunk / kWave;
+
+template <int IB>
+__global__ __launch_bounds__(64) void perm_count(const void* idx, int T, int k, int E,
+                                                 int nbits, int V, int nblk, int32_t* hist,
+                                                 int32_t* lrank) {
+  __shared__ int run[1024];
+  const int lane = lane_id();
+  for (int e = lane; e < E; e += kWave) run[e] = 0;
+  __syncthreads();
+  const int b = blockIdx.x;
+  int ee[kRounds], rk[kRounds];
+  rank_chunk<IB, kRounds>(idx, T, k, E, nbits, V, b * kPermChunk, run, ee, rk);
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int v = b * kPermChunk + r * kWave + lane;
+    if (v < V) lrank[v] = rk[r];
+  }
+  __syncthreads();
+  for (int e = lane; e < E; e += kWave) hist[static_cast<int64_t>(e) * nblk + b] = run[e];
+}
+
+// Exclusive scan of n ints in place order (one workgroup of 1024 threads).
+__global__ __launch_bounds__(1024) void perm_scan(const int32_t* hist, int E, int nblk, int V,
+                                                  int32_t* base, int32_t* counts,
+                                                  int32_t* offsets) {
+  __shared__ int wsum[16];
+  const int n = E * nblk;
+  const int tid = threadIdx.x;
+  const int per = (n + 1023) / 1024;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  int local = 0;
+  for (int i = lo; i < hi; ++i) local += hist[i];
+  // inclusive scan of `local` across the block
+  int incl = local;
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < 16 ? wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(w, o, kWave);
+      if (lane >= o) w += y;
+    }
+    if (lane < 16) wsum[lane] = w;
+  }
+  __syncthreads();
+  int run = incl - local + (wave > 0 ? wsum[wave - 1] : 0);
+  for (int i = lo; i < hi; ++i) {
+    base[i] = run;
+    run += hist[i];
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    const int o0 = base[static_cast<int64_t>(e) * nblk];
+    const int o1 = (e + 1 < E) ? base[static_cast<int64_t>(e + 1) * nblk] : wsum[15];
+    offsets[e] = o0;
+    counts[e] = o1 - o0;
+  }
+  if (tid == 0) offsets[E] = wsum[15];
+}
+
+template <int IB>
+__global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k, int E, int V,
+                                                   int nblk, const int32_t* base,
+                                                   const int32_t* lrank, int32_t* perm_tok,
+                                                   int32_t* perm_slot, int32_t* inv) {
+  const int lane = lane_id();
+  const int b = blockIdx.x;
+  for (int r = 0; r < kRounds; ++r) {
+    const int v = b * kPermChunk + r * kWave + lane;
+    if (v >= V) break;
+    const int s = v / T;
+    const int t = v - s * T;
+    const int e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
+    const int64_t ts = static_cast<int64_t>(t) * k + s;
+    if (e < 0 || e >= E) {
+      inv[ts] = -1;
+      continue;
+    }
+    const int pos = base[static_cast<int64_t>(e) * nblk + b] + lrank[v];
+    perm_tok[pos] = t;
+    perm_slot[pos] = s;
+    inv[ts] = pos;
+  }
+}
+
+// Whole permutation in one wave when V <= kPermChunk (decode-sized batches).
+template <int IB>
+__global__ __launch_bounds__(64) void perm_single(const void* idx, int T, int k, int E,
+                                                  int nbits, int V, int32_t* counts,
+                                                  int32_t* offsets, int32_t* perm_tok,
+                                                  int32_t* perm_slot, int32_t* inv) {
+  __shared__ int run[1024];
+  __shared__ int start[1024];
+  const int lane = lane_id();
+  for (int e = lane; e < E; e += kWave) run[e] = 0;
+  __syncthreads();
+  int ee[kRounds], rk[kRounds];
+  rank_chunk<IB, kRounds>(idx, T, k, E, nbits, V, 0, run, ee, rk);
+  __syncthreads();
+  // exclusive scan of run[0..E) by one wave: each lane owns a contiguous slice
+  const int per = (E + kWave - 1) / kWave;
+  const int lo = min(E, lane * per), hi = min(E, lo + per);
+  int local = 0;
+  for (int e = lo; e < hi; ++e) local += run[e];
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  int acc = incl - local;
+  for (int e = lo; e < hi; ++e) {
+    start[e] = acc;
+    offsets[e] = acc;
+    counts[e] = run[e];
+    acc += run[e];
+  }
+  if (lane == 63) offsets[E] = incl;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int v = r * kWave + lane;
+    if (v < V) {
+      const int s = v / T;
+      const int t = v - s * T;
+      const int64_t ts = static_cast<int64_t>(t) * k + s;
+      if (ee[r] < 0) {
+        inv[ts] = -1;
+      } else {
+        const int pos = start[ee[r]] + rk[r];
+        perm_tok[pos] = t;
+        perm_slot[pos] = s;
+        inv[ts] = pos;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t value) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = value;
+}
+
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  fill_i32_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(p, n, value);
+  return hipGetLastError();
+}
+
+static int bits_for(int E) {
+  int n = 0;
+  while ((1 << n) < E) ++n;
+  return n;
+}
+
+template <int IB>
+static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int32_t* counts,
+                                   int32_t* offsets, int32_t* perm_tok, int32_t* perm_slot,
+                                   int32_t* inv, int32_t* hist, int32_t* base, int32_t* lrank,
+                                   hipStream_t s) {
+  const int V = static_cast<int>(T * k);
+  const int nbits = bits_for(E);
+  if (V <= kPermChunk) {
+    perm_single<IB><<<1, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, counts, offsets,
+                                     perm_tok, perm_slot, inv);
+    return hipGetLastError();
+  }
+  const int nblk = static_cast<int>(perm_blocks(V));
+  perm_count<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist,
+                                     lrank);
+  perm_scan<<<1, 1024, 0, s>>>(hist, E, nblk, V, base, counts, offsets);
+  perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, lrank,
+                                       perm_tok, perm_slot, inv);
+  return hipGetLastError();
+}
+
+hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int E,
+                          bool /*shared_rows*/, int32_t* counts, int32_t* offsets,
+                          int32_t* perm_tok, int32_t* perm_slot, int32_t* inv, int32_t* hist,
+                          int32_t* base, int32_t* lrank, hipStream_t s) {
+  if (idx_bytes == 8)
+    return launch_permute_t<8>(idx, T, k, E, counts, offsets, perm_tok, perm_slot, inv, hist,
+                               base, lrank, s);
+  return launch_permute_t<4>(idx, T, k, E, counts, offsets, perm_tok, perm_slot, inv, hist,
+                             base, lrank, s);
+}
+
+}  // namespace lbmoe

@@ -1,0 +1,287 @@
+"""Drop-in MoE modules backed by the gfx950 HIP library (liblbmoe.so).
+
+Same class names, constructor arguments, parameter names, shapes and return values as the
+reference's MoE classes in nanovllm/models/qwen3_5.py:
+
+* Qwen3_5TopKRouter       qwen3_5.py:754-774   forward(x) -> (top_k_weights bf16, top_k_indices int64)
+* Qwen3_5Experts          qwen3_5.py:781-874   forward(x, idx, w) -> [T,H]
+* Qwen3_5SparseMoeBlock   qwen3_5.py:881-905   forward(x) -> [T,H]
+* Qwen3_5SharedExpertMLP  qwen3_5.py:908-917   forward(x) -> [T,H]
+
+so the reference's weight loader (nanovllm/utils/loader.py:16-61, plain ``param.data.copy_``)
+and decoder layer (qwen3_5.py:956-962, :1004) use them unchanged. Differences, all deliberate:
+
+* One algorithm for every batch size (the reference switches between a dense gather+bmm for
+  decode and a per-expert loop for prefill on ``get_context().is_prefill``,
+  qwen3_5.py:808-813); the flag is not read.
+* Tie order of equal router probabilities is (descending logit, ascending expert index);
+  torch.topk leaves it implementation-defined.
+* ``shared_expert_intermediate_size == 0`` builds no shared expert (the reference always
+  builds one).
+* ``Qwen3_5TopKRouter.logit_bias`` (default None) is an optional fp32 [E] tensor added to
+  the upcast logits before the softmax; it is not a checkpoint parameter.
+* ``Qwen3_5SparseMoeBlock.quantize_fp8_()`` converts the expert and shared-expert weights to
+  OCP e4m3fn with per-128x128-block fp32 scales (no counterpart in the reference).
+
+Every forward runs on the tensor's CUDA (HIP) device on the current stream, enqueues HIP
+kernels only (no host synchronisation), and raises RuntimeError for CPU tensors, wrong dtypes
+or a missing library build.
+"""
+import ctypes
+
+import torch
+from torch import nn
+
+from . import _lib
+from ._lib import LbmoeLayer, check, lib, ptr
+
+__all__ = ["Qwen3_5TopKRouter", "Qwen3_5Experts", "Qwen3_5SharedExpertMLP",
+           "Qwen3_5SparseMoeBlock"]
+
+
+def _require(t, name, dtype=torch.bfloat16, ndim=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} is on {t.device}: the MoE layer runs only on a gfx950 GPU")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise RuntimeError(f"{name} must have {ndim} dims, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _workspace(layer, T, device):
+    return torch.empty(_lib.workspace_size(layer, T), dtype=torch.uint8, device=device)
+
+
+class Qwen3_5TopKRouter(nn.Module):
+    """Router: softmax over bf16 logits, top-k, renormalise, cast to bf16 (qwen3_5.py:754-774).
+
+    Weight: gate.weight [num_experts, hidden_size].
+    """
+
+    def __init__(self, num_experts: int, hidden_size: int, top_k: int):
+        super().__init__()
+        self.top_k = top_k
+        self.num_experts = num_experts
+        self.weight = nn.Parameter(torch.zeros(num_experts, hidden_size))
+        self.logit_bias = None
+
+    def _layer(self):
+        E, H = self.weight.shape
+        L = LbmoeLayer()
+        L.hidden_size, L.num_experts, L.top_k = H, E, self.top_k
+        L.moe_intermediate_size = 128           # routed-expert sizes are unused by the router
+        L.gate_weight = self.weight.data_ptr()
+        if self.logit_bias is not None:
+            _require(self.logit_bias, "logit_bias", torch.float32, 1)
+            L.logit_bias = self.logit_bias.data_ptr()
+        return L
+
+    def logits(self, hidden_states):
+        """bf16 router logits [T, E] (the F.linear of qwen3_5.py:769)."""
+        _require(hidden_states, "hidden_states", ndim=2)
+        _require(self.weight, "gate.weight", ndim=2)
+        T = hidden_states.shape[0]
+        out = torch.empty((T, self.num_experts), dtype=torch.bfloat16, device=hidden_states.device)
+        L = self._layer()
+        with torch.cuda.device(hidden_states.device):
+            check(lib().lbmoe_router_logits(ctypes.byref(L), ptr(hidden_states), T, ptr(out),
+                                            _lib.stream_of(hidden_states.device)),
+                  "lbmoe_router_logits")
+        return out
+
+    def forward(self, hidden_states: torch.Tensor):
+        logits = self.logits(hidden_states)
+        T = hidden_states.shape[0]
+        dev = hidden_states.device
+        w = torch.empty((T, self.top_k), dtype=torch.bfloat16, device=dev)
+        idx = torch.empty((T, self.top_k), dtype=torch.int64, device=dev)
+        L = self._layer()
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_route(ctypes.byref(L), ptr(logits), None, T, ptr(idx), 8, ptr(w),
+                                    None, _lib.stream_of(dev)), "lbmoe_route")
+        return w, idx
+
+
+class Qwen3_5Experts(nn.Module):
+    """Fused expert weights stored as 3-D tensors (qwen3_5.py:781-800).
+
+    - experts.gate_up_proj  [num_experts, 2 * moe_intermediate_size, hidden_size]
+    - experts.down_proj     [num_experts, hidden_size, moe_intermediate_size]
+    """
+
+    def __init__(self, num_experts: int, hidden_size: int, moe_intermediate_size: int):
+        super().__init__()
+        self.num_experts = num_experts
+        self.hidden_size = hidden_size
+        self.intermediate_size = moe_intermediate_size
+        self.gate_up_proj = nn.Parameter(
+            torch.empty(num_experts, 2 * moe_intermediate_size, hidden_size))
+        self.down_proj = nn.Parameter(
+            torch.empty(num_experts, hidden_size, moe_intermediate_size))
+        self.weight_dtype = _lib.LBMOE_W_BF16
+        self.gate_up_q = self.gate_up_scale = self.down_q = self.down_scale = None
+
+    def fill_layer(self, L):
+        L.num_experts = self.num_experts
+        L.hidden_size = self.hidden_size
+        L.moe_intermediate_size = self.intermediate_size
+        L.weight_dtype = self.weight_dtype
+        if self.weight_dtype == _lib.LBMOE_W_FP8_E4M3:
+            L.gate_up_proj = self.gate_up_q.data_ptr()
+            L.down_proj = self.down_q.data_ptr()
+            L.gate_up_scale = self.gate_up_scale.data_ptr()
+            L.down_scale = self.down_scale.data_ptr()
+        else:
+            _require(self.gate_up_proj, "experts.gate_up_proj", ndim=3)
+            _require(self.down_proj, "experts.down_proj", ndim=3)
+            L.gate_up_proj = self.gate_up_proj.data_ptr()
+            L.down_proj = self.down_proj.data_ptr()
+
+    def forward(self, hidden_states, top_k_indices, top_k_weights):
+        _require(hidden_states, "hidden_states", ndim=2)
+        _require(top_k_indices, "top_k_indices", None, 2)
+        _require(top_k_weights, "top_k_weights", torch.bfloat16, 2)
+        if top_k_indices.dtype not in (torch.int64, torch.int32):
+            raise RuntimeError(f"top_k_indices must be int64 or int32, got {top_k_indices.dtype}")
+        T, k = top_k_indices.shape
+        if hidden_states.shape[0] != T or tuple(top_k_weights.shape) != (T, k):
+            raise RuntimeError("hidden_states / top_k_indices / top_k_weights disagree on [T, k]")
+        L = LbmoeLayer()
+        self.fill_layer(L)
+        L.top_k = k
+        dev = hidden_states.device
+        y = torch.empty_like(hidden_states)
+        ws = _workspace(L, T, dev)
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_experts(ctypes.byref(L), ptr(hidden_states), ptr(top_k_indices),
+                                      top_k_indices.element_size(), ptr(top_k_weights), T, ptr(y),
+                                      ptr(ws), ws.numel(), _lib.stream_of(dev)), "lbmoe_experts")
+        return y
+
+
+class Qwen3_5SharedExpertMLP(nn.Module):
+    """Dense SwiGLU MLP: down(silu(gate_proj x) * up_proj x) (qwen3_5.py:908-917)."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+        self.weight_dtype = _lib.LBMOE_W_BF16
+        self.q = None   # fp8: dict name -> (codes, scales)
+
+    def _ptrs(self):
+        if self.weight_dtype == _lib.LBMOE_W_FP8_E4M3:
+            q = self.q
+            return ([q[n][0].data_ptr() for n in ("gate", "up", "down")],
+                    [q[n][1].data_ptr() for n in ("gate", "up", "down")])
+        for n, m in (("gate_proj", self.gate_proj), ("up_proj", self.up_proj),
+                     ("down_proj", self.down_proj)):
+            _require(m.weight, f"shared_expert.{n}.weight", ndim=2)
+        return ([self.gate_proj.weight.data_ptr(), self.up_proj.weight.data_ptr(),
+                 self.down_proj.weight.data_ptr()], [None, None, None])
+
+    def fill_layer(self, L):
+        L.shared_intermediate_size = self.gate_proj.weight.shape[0]
+        (g, u, d), (gs, us, ds) = self._ptrs()
+        L.shared_gate_proj, L.shared_up_proj, L.shared_down_proj = g, u, d
+        L.shared_gate_scale, L.shared_up_scale, L.shared_down_scale = gs, us, ds
+
+    def forward(self, x):
+        _require(x, "x", ndim=2)
+        T, H = x.shape
+        Is = self.gate_proj.weight.shape[0]
+        (g, u, d), (gs, us, ds) = self._ptrs()
+        n = ctypes.c_size_t(0)
+        check(lib().lbmoe_dense_mlp_workspace_size(H, Is, self.weight_dtype, T, ctypes.byref(n)),
+              "lbmoe_dense_mlp_workspace_size")
+        dev = x.device
+        ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
+        out = torch.empty_like(x)
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_dense_mlp(g, u, d, gs, us, ds, H, Is, self.weight_dtype, ptr(x), T,
+                                        ptr(out), ptr(ws), ws.numel(), _lib.stream_of(dev)),
+                  "lbmoe_dense_mlp")
+        return out
+
+
+def _quantize_blocks(w):
+    """bf16 [..., N, K] -> (e4m3 codes as uint8, fp32 scales [..., N/128, K/128]) on the GPU."""
+    _require(w, "weight")
+    *lead, N, K = w.shape
+    batch = 1
+    for d in lead:
+        batch *= d
+    q = torch.empty(w.shape, dtype=torch.uint8, device=w.device)
+    s = torch.empty((*lead, N // 128, K // 128), dtype=torch.float32, device=w.device)
+    with torch.cuda.device(w.device):
+        check(lib().lbmoe_quantize_fp8_blocks(ptr(w), batch, N, K, ptr(q), ptr(s),
+                                              _lib.stream_of(w.device)),
+              "lbmoe_quantize_fp8_blocks")
+    return q, s
+
+
+class Qwen3_5SparseMoeBlock(nn.Module):
+    """Router + routed experts + gated shared expert (qwen3_5.py:881-905)."""
+
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 moe_intermediate_size: int, shared_expert_intermediate_size: int):
+        super().__init__()
+        self.gate = Qwen3_5TopKRouter(num_experts, hidden_size, num_experts_per_tok)
+        self.experts = Qwen3_5Experts(num_experts, hidden_size, moe_intermediate_size)
+        if shared_expert_intermediate_size > 0:
+            self.shared_expert = Qwen3_5SharedExpertMLP(hidden_size,
+                                                        shared_expert_intermediate_size)
+            self.shared_expert_gate = nn.Linear(hidden_size, 1, bias=False)
+        else:
+            self.shared_expert = None
+            self.shared_expert_gate = None
+
+    def layer(self):
+        """The lbmoe_layer struct describing this block's parameters."""
+        L = self.gate._layer()
+        self.experts.fill_layer(L)
+        L.top_k = self.gate.top_k
+        if self.shared_expert is not None:
+            self.shared_expert.fill_layer(L)
+            _require(self.shared_expert_gate.weight, "shared_expert_gate.weight", ndim=2)
+            L.shared_expert_gate = self.shared_expert_gate.weight.data_ptr()
+            if self.shared_expert.weight_dtype != self.experts.weight_dtype:
+                raise RuntimeError("experts and shared expert must use the same weight dtype")
+        return L
+
+    def workspace_size(self, T):
+        return _lib.workspace_size(self.layer(), T)
+
+    def forward(self, hidden_states: torch.Tensor, workspace: torch.Tensor = None):
+        _require(hidden_states, "hidden_states", ndim=2)
+        T = hidden_states.shape[0]
+        L = self.layer()
+        dev = hidden_states.device
+        if workspace is None:
+            workspace = _workspace(L, T, dev)
+        y = torch.empty_like(hidden_states)
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_forward(ctypes.byref(L), ptr(hidden_states), T, ptr(y),
+                                      ptr(workspace), workspace.numel(), _lib.stream_of(dev)),
+                  "lbmoe_forward")
+        return y
+
+    @torch.no_grad()
+    def quantize_fp8_(self):
+        """Convert expert (and shared-expert) weights to e4m3fn + 128x128 block scales."""
+        ex = self.experts
+        ex.gate_up_q, ex.gate_up_scale = _quantize_blocks(ex.gate_up_proj)
+        ex.down_q, ex.down_scale = _quantize_blocks(ex.down_proj)
+        ex.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+        if self.shared_expert is not None:
+            se = self.shared_expert
+            se.q = {"gate": _quantize_blocks(se.gate_proj.weight),
+                    "up": _quantize_blocks(se.up_proj.weight),
+                    "down": _quantize_blocks(se.down_proj.weight)}
+            se.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+        return self

@@ -1,0 +1,191 @@
+"""GPU parity of every stage of the HIP MoE layer against the CPU oracle (through the C ABI)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from layerbatch_amd import _lib
+from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
+from layerbatch_amd.synth import MoEShape, SHAPES, make_layer, make_x, zipf_bias
+from oracle import moe as om
+from tests import gpu_checks as gc
+from tests.helpers import bf16_bits_of, layer_np, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _block(shape, w, device):
+    H, E, k, I, Is = (shape.hidden_size, shape.num_experts, shape.top_k,
+                      shape.moe_intermediate_size, shape.shared_expert_intermediate_size)
+    blk = Qwen3_5SparseMoeBlock(H, E, k, I, Is).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        blk.gate.weight.copy_(w["gate"])
+        blk.experts.gate_up_proj.copy_(w["gate_up"])
+        blk.experts.down_proj.copy_(w["down"])
+        if Is:
+            blk.shared_expert.gate_proj.weight.copy_(w["sh_gate"])
+            blk.shared_expert.up_proj.weight.copy_(w["sh_up"])
+            blk.shared_expert.down_proj.weight.copy_(w["sh_down"])
+            blk.shared_expert_gate.weight.copy_(w["sh_gate_w"])
+    return blk
+
+
+def _region(blk, ws, T, name, dtype, shape):
+    off, nb = _lib.workspace_region(blk.layer(), T, name)
+    n = int(np.prod(shape))
+    esz = torch.empty((), dtype=dtype).element_size()
+    assert n * esz <= nb
+    return ws[off:off + n * esz].view(dtype).view(shape)
+
+
+def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu"):
+    w, g = make_layer(shape, seed=seed, device=gen_device)
+    x = make_x(g, T, shape.hidden_size, device=gen_device)
+    wd = {k_: v.to(device) for k_, v in w.items()}
+    blk = _block(shape, wd, device)
+    if bias is not None:
+        blk.gate.logit_bias = bias.to(device)
+    xd = x.to(device)
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=device)
+    y = blk(xd, workspace=ws)
+    torch.cuda.synchronize()
+    E, k = shape.num_experts, shape.top_k
+    logits = _region(blk, ws, T, "logits", torch.bfloat16, (T, E))
+    idx = _region(blk, ws, T, "topk_idx", torch.int32, (T, k))
+    topw = _region(blk, ws, T, "topk_w", torch.bfloat16, (T, k))
+    wn = layer_np(w)
+    xn = to_np(x)
+    gc.check_logits(bf16_bits_of(logits), xn, wn["gate"])
+    bn = None if bias is None else bias.cpu().numpy()
+    w_ref, idx_ref = gc.check_route(to_np(idx), bf16_bits_of(topw), to_np(logits), bn, k)
+    V = T * k
+    gc.check_permutation(idx_ref, E,
+                         to_np(_region(blk, ws, T, "counts", torch.int32, (E,))),
+                         to_np(_region(blk, ws, T, "offsets", torch.int32, (E + 1,))),
+                         to_np(_region(blk, ws, T, "perm_tok", torch.int32, (V,))),
+                         to_np(_region(blk, ws, T, "perm_slot", torch.int32, (V,))),
+                         to_np(_region(blk, ws, T, "inv", torch.int32, (T, k))))
+    y_ref = gc.block_reference(xn, wn, idx_ref, to_np(topw), k,
+                               shared=True if shape.shared_expert_intermediate_size else None)
+    return gc.check_output(to_np(y), y_ref, gc.TOL_BF16)
+
+
+def test_block_small_layer(gpu):
+    """H=1024, E=16, top-2, I=512, T=64 (seed 0)."""
+    _run_and_check(SHAPES["small-h1024-e16"], 64, gpu)
+
+
+@pytest.mark.parametrize("T", [1, 3, 17, 128, 300])
+def test_block_small_layer_sizes(gpu, T):
+    _run_and_check(SHAPES["small-h1024-e16"], T, gpu, seed=T)
+
+
+def test_block_with_shared_expert(gpu):
+    shape = MoEShape(1024, 32, 4, 256, 384)
+    _run_and_check(shape, 40, gpu, seed=3)
+
+
+def test_block_with_bias(gpu):
+    shape = MoEShape(1024, 64, 6, 256, 0)
+    g = torch.Generator().manual_seed(11)
+    _run_and_check(shape, 200, gpu, seed=5, bias=zipf_bias(g, 64))
+
+
+def test_dense_reduction_e1_k1(gpu):
+    """k = 1, E = 1: the block is a dense SwiGLU MLP with weight 1."""
+    shape = MoEShape(256, 1, 1, 256, 0)
+    _run_and_check(shape, 33, gpu, seed=9)
+
+
+@pytest.mark.parametrize("T,k,E,ib", [(1, 1, 1, 4), (7, 2, 16, 8), (128, 8, 128, 4),
+                                      (129, 8, 128, 8), (1000, 10, 512, 4), (8192, 8, 128, 4),
+                                      (3000, 7, 1000, 8), (0, 4, 16, 4)])
+def test_permute_exact(gpu, lbmoe, T, k, E, ib):
+    rng = np.random.default_rng(T * 131 + k)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]) if T else np.zeros((0, k), np.int64)
+    if T > 10:
+        idx[3, 0] = E          # out of range: dropped, inv = -1
+        idx[5, k - 1] = -1
+    dt = torch.int32 if ib == 4 else torch.int64
+    d_idx = torch.tensor(idx, dtype=dt, device=gpu).reshape(T, k)
+    V = T * k
+    counts = torch.empty(E, dtype=torch.int32, device=gpu)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=gpu)
+    pt = torch.full((max(V, 1),), -7, dtype=torch.int32, device=gpu)
+    ps = torch.full((max(V, 1),), -7, dtype=torch.int32, device=gpu)
+    inv = torch.empty((max(V, 1),), dtype=torch.int32, device=gpu)
+    n = ctypes.c_size_t(0)
+    _lib.check(lbmoe.lbmoe_permute_workspace_size(T, k, E, ctypes.byref(n)), "ws")
+    ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=gpu)
+    _lib.check(lbmoe.lbmoe_permute(_lib.ptr(d_idx), ib, T, k, E, _lib.ptr(counts), _lib.ptr(offsets),
+                                   _lib.ptr(pt), _lib.ptr(ps), _lib.ptr(inv), _lib.ptr(ws), n.value,
+                                   _lib.stream_of(gpu)), "lbmoe_permute")
+    torch.cuda.synchronize()
+    c_ref, o_ref, pt_ref, ps_ref, inv_ref = _perm_ref_with_drops(idx, E)
+    np.testing.assert_array_equal(counts.cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), o_ref)
+    nv = int(o_ref[-1])
+    np.testing.assert_array_equal(pt.cpu().numpy()[:nv], pt_ref)
+    np.testing.assert_array_equal(ps.cpu().numpy()[:nv], ps_ref)
+    if V:
+        np.testing.assert_array_equal(inv.cpu().numpy()[:V].reshape(T, k), inv_ref)
+
+
+def _perm_ref_with_drops(idx, E):
+    """Oracle permutation where out-of-range ids are dropped (inv = -1)."""
+    T, k = idx.shape
+    valid = (idx >= 0) & (idx < E)
+    e_sm = idx.T.reshape(-1)
+    v_ok = valid.T.reshape(-1)
+    order = [v for v in np.argsort(np.where(v_ok, e_sm, E), kind="stable") if v_ok[v]]
+    order = np.asarray(order, np.int64)
+    counts = np.bincount(e_sm[v_ok], minlength=E)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    inv_sm = np.full(T * k, -1, np.int64)
+    inv_sm[order] = np.arange(order.size)
+    return counts, offsets, order % max(T, 1), order // max(T, 1), inv_sm.reshape(k, T).T
+
+
+def test_router_module_returns_reference_types(gpu):
+    shape = SHAPES["small-h1024-e16"]
+    w, g = make_layer(shape, device="cpu")
+    x = make_x(g, 64, shape.hidden_size).to(gpu)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    tw, ti = blk.gate(x)
+    assert tw.dtype == torch.bfloat16 and ti.dtype == torch.int64
+    assert tuple(tw.shape) == (64, 2) and tuple(ti.shape) == (64, 2)
+    logits = to_np(blk.gate.logits(x))
+    gc.check_route(ti.cpu().numpy(), bf16_bits_of(tw), logits, None, 2)
+    # the experts module takes the router's int64 indices (qwen3_5.py:901-902)
+    y = blk.experts(x, ti, tw)
+    wn = layer_np(w)
+    y_ref = om.experts(to_np(x), ti.cpu().numpy(), to_np(tw), wn["gate_up"], wn["down"])
+    gc.check_output(to_np(y), y_ref, gc.TOL_BF16)
+
+
+def test_shared_expert_mlp_module(gpu):
+    shape = MoEShape(1024, 8, 2, 128, 384)
+    w, g = make_layer(shape, seed=4)
+    x = make_x(g, 50, 1024)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    out = blk.shared_expert(x.to(gpu))
+    wn = layer_np(w)
+    ref = om.shared_expert(to_np(x), wn["sh_gate"], wn["sh_up"], wn["sh_down"])
+    gc.check_output(to_np(out), ref, gc.TOL_BF16)
+
+
+def test_zero_tokens(gpu):
+    shape = SHAPES["small-h1024-e16"]
+    w, _ = make_layer(shape)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    y = blk(torch.empty((0, 1024), dtype=torch.bfloat16, device=gpu))
+    assert y.shape == (0, 1024)
+
+
+def test_cpu_tensor_raises(gpu):
+    shape = SHAPES["small-h1024-e16"]
+    w, _ = make_layer(shape)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    with pytest.raises(RuntimeError):
+        blk(torch.zeros((4, 1024), dtype=torch.bfloat16))
