@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""Benchmark of the MoE feed-forward layer on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--T 128] [--prefill-T 8192] [--no-cpu-baseline]
+
+Headline workload: the Qwen3-30B-A3B MoE layer (H=2048, E=128, top-8, I=768, bf16 weights
+~N(0,0.02), activations ~N(0,1), synthetic, seed 0) at decode T=128. One step is one call of
+the whole layer (router -> permute -> gate_up+SiLU*mul -> down -> combine) on inputs already
+resident in HBM. The same run also measures the prefill chunk T=8192 with a Zipf(1.2)
+router bias (skewed expert loads).
+
+Printed: one JSON line. `value` is the layer's algorithmic HBM throughput in GB/s at T=128
+(hit experts' weights + router weight + x in + y out, divided by the wall time per call).
+`roofline` describes the dominant kernel (gate_up), timed with HIP events recorded on the
+library's stream around that kernel in every timed call. `cpu_baseline` times the torch-CPU
+restatement of the reference's decode algorithm (dense gather + bmm) on the host's cores.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("MoE layer µs/call + TFLOP/s (or GB/s) & % roofline, decode T=128 / "
+          "prefill T=8192")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--T", type=int, default=128)
+    p.add_argument("--prefill-T", type=int, default=8192)
+    p.add_argument("--shape", default="qwen3-30b-a3b")
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    return p.parse_args()
+
+
+class HipEvents:
+    """hipEvent_t helpers through the HIP runtime torch has loaded."""
+
+    def __init__(self):
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64" in line:
+                    path = line.split()[-1]
+                    break
+        self.h = ctypes.CDLL(path or "libamdhip64.so.7")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        evs = (ctypes.c_void_p * n)()
+        for i in range(n):
+            e = ctypes.c_void_p()
+            assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+            evs[i] = e
+        return evs
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        assert self.h.hipEventSynchronize(b) == 0
+        assert self.h.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+def layer_inputs(shape, T, seed, zipf, device):
+    import torch
+    from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
+    from layerbatch_amd.synth import make_layer, make_x, zipf_bias
+    w, g = make_layer(shape, seed=seed, device=device)
+    x = make_x(g, T, shape.hidden_size, device=device)
+    blk = Qwen3_5SparseMoeBlock(shape.hidden_size, shape.num_experts, shape.top_k,
+                                shape.moe_intermediate_size, shape.shared_expert_intermediate_size)
+    blk = blk.to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        blk.gate.weight.copy_(w["gate"])
+        blk.experts.gate_up_proj.copy_(w["gate_up"])
+        blk.experts.down_proj.copy_(w["down"])
+        if shape.shared_expert_intermediate_size:
+            blk.shared_expert.gate_proj.weight.copy_(w["sh_gate"])
+            blk.shared_expert.up_proj.weight.copy_(w["sh_up"])
+            blk.shared_expert.down_proj.weight.copy_(w["sh_down"])
+            blk.shared_expert_gate.weight.copy_(w["sh_gate_w"])
+    if zipf:
+        blk.gate.logit_bias = zipf_bias(g, shape.num_experts, device=device)
+    del w
+    return blk, x
+
+
+def measure(blk, x, steps, warmup, hip):
+    """Wall time per call over `steps` plain calls, then per-stage HIP-event times over
+    `steps` profiled calls. Returns a dict of timings and routing statistics."""
+    import torch
+    from layerbatch_amd import _lib
+    T = x.shape[0]
+    L = blk.layer()
+    ws = torch.empty(_lib.workspace_size(L, T), dtype=torch.uint8, device=x.device)
+    y = torch.empty_like(x)
+    lib = _lib.lib()
+    stream = _lib.stream_of(x.device)
+    args = (ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws), ws.numel(), stream)
+    for _ in range(warmup):
+        _lib.check(lib.lbmoe_forward(*args), "lbmoe_forward")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lib.lbmoe_forward(*args)
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) / steps * 1e6
+
+    n_ev = _lib.LBMOE_PROFILE_EVENTS
+    evsets = [hip.create(n_ev) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for evs in evsets:
+        _lib.check(lib.lbmoe_forward_profiled(*args, evs, n_ev), "lbmoe_forward_profiled")
+    torch.cuda.synchronize()
+    stages = {name: 0.0 for name in _lib.PROFILE_STAGES}
+    for evs in evsets:
+        for i, name in enumerate(_lib.PROFILE_STAGES):
+            stages[name] += hip.elapsed_ms(evs[i], evs[i + 1]) * 1e3 / steps
+    off, nb = _lib.workspace_region(L, T, "counts")
+    counts = ws[off:off + 4 * blk.gate.num_experts].view(torch.int32).cpu()
+    return {"wall_us": wall_us, "stage_us": stages, "hit_experts": int((counts > 0).sum()),
+            "max_tokens_per_expert": int(counts.max()), "y": y}
+
+
+def work(shape, T, n_hit):
+    """Algorithmic bytes/flops of the layer and of its gate_up kernel."""
+    H, E, k, I, Is = (shape.hidden_size, shape.num_experts, shape.top_k,
+                      shape.moe_intermediate_size, shape.shared_expert_intermediate_size)
+    wb = 2
+    layer_bytes = n_hit * 3 * H * I * wb + (3 * H * Is * wb + H * 2 if Is else 0) + E * H * 2 + 2 * T * H * 2
+    layer_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * E * H
+    gu_bytes = n_hit * 2 * I * H * wb + (2 * Is * H * wb if Is else 0) + T * H * 2 + (T * k * I + (T * Is if Is else 0)) * 2
+    gu_flops = 2 * T * k * 2 * H * I + 2 * T * 2 * H * Is
+    return layer_bytes, layer_flops, gu_bytes, gu_flops
+
+
+def cpu_baseline(blk, x, zipf, budget_s):
+    """The torch-CPU restatement of the reference path on this host's cores."""
+    import torch
+    from oracle import torch_ref
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    wg = blk.gate.weight.detach().cpu()
+    wgu = blk.experts.gate_up_proj.detach().cpu()
+    wd = blk.experts.down_proj.detach().cpu()
+    bias = None if blk.gate.logit_bias is None else blk.gate.logit_bias.cpu()
+    xc = x.cpu()
+    algorithm = "sparse" if zipf or x.shape[0] > 512 else "dense"
+    k = blk.gate.top_k
+    times = []
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        torch_ref.block(xc, wg, wgu, wd, k, bias=bias, algorithm=algorithm)       # warmup
+        first = time.perf_counter() - t0
+        n = max(1, min(5, int(budget_s / max(first, 1e-3))))
+        for _ in range(n):
+            t0 = time.perf_counter()
+            torch_ref.block(xc, wg, wgu, wd, k, bias=bias, algorithm=algorithm)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return {"us_per_call": times[len(times) // 2] * 1e6, "cores": ncores, "calls": len(times),
+            "algorithm": algorithm}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the MoE layer is "
+              "measured at one GPU's share and no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from layerbatch_amd.synth import SHAPES
+    dev = torch.device("cuda:0")
+    hip = HipEvents()
+    shape = SHAPES[args.shape]
+
+    blk, x = layer_inputs(shape, args.T, 0, False, dev)
+    d = measure(blk, x, args.steps, args.warmup, hip)
+    lb, lf, gb, gf = work(shape, args.T, d["hit_experts"])
+    gu_us = d["stage_us"]["gate_up"]
+    gu_gbs = gb / (gu_us * 1e-6) / 1e9
+    layer_gbs = lb / (d["wall_us"] * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        c = cpu_baseline(blk, x, False, args.cpu_budget_s)
+        cpu = {"value": round(lb / (c["us_per_call"] * 1e-6) / 1e9, 3), "unit": "GB/s",
+               "cores": c["cores"], "kind": "port",
+               "us_per_call": round(c["us_per_call"], 1),
+               "sample": f"{c['calls']} timed calls (median, after 1 warmup) of the torch-CPU "
+                         f"restatement of the reference's {c['algorithm']} decode algorithm at "
+                         f"the same T={args.T} on the same inputs"}
+    del blk, x
+    torch.cuda.empty_cache()
+
+    prefill = None
+    if not args.no_prefill:
+        pblk, px = layer_inputs(shape, args.prefill_T, 0, True, dev)
+        steps = max(3, args.steps // 5)
+        p = measure(pblk, px, steps, max(1, args.warmup // 5), hip)
+        plb, plf, pgb, pgf = work(shape, args.prefill_T, p["hit_experts"])
+        pgu = p["stage_us"]["gate_up"]
+        prefill = {
+            "T": args.prefill_T, "router_bias": "zipf(1.2)", "us_per_call": round(p["wall_us"], 1),
+            "tflops": round(plf / (p["wall_us"] * 1e-6) / 1e12, 2),
+            "frac_of_bf16_mfma_peak": round(plf / (p["wall_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "hit_experts": p["hit_experts"], "max_tokens_per_expert": p["max_tokens_per_expert"],
+            "stage_us": {k_: round(v, 1) for k_, v in p["stage_us"].items()},
+            "gate_up_tflops": round(pgf / (pgu * 1e-6) / 1e12, 2),
+        }
+        del pblk, px
+
+    out = {
+        "metric": METRIC, "value": round(layer_gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(d["wall_us"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seed 0, weights ~N(0,0.02), activations ~N(0,1), random init)",
+        "config": {"workload": f"{args.shape} MoE layer decode", "hidden_size": shape.hidden_size,
+                   "num_experts": shape.num_experts, "top_k": shape.top_k,
+                   "moe_intermediate_size": shape.moe_intermediate_size,
+                   "shared_expert_intermediate_size": shape.shared_expert_intermediate_size,
+                   "T": args.T, "weights": "bf16"},
+        "us_per_call": round(d["wall_us"], 2),
+        "layer_frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "hit_experts": d["hit_experts"],
+        "stage_us": {k_: round(v, 2) for k_, v in d["stage_us"].items()},
+        "roofline": {"kernel": "gate_up_bf16_kernel", "bound": "hbm", "achieved": round(gu_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": gb,
+                     "avg_launch_us": round(gu_us, 2)},
+        "cpu_baseline": cpu,
+        "prefill": prefill,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -102,6 +102,20 @@ int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t regi
 int32_t lbmoe_forward(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Number of events lbmoe_forward_profiled records. */
+#define LBMOE_PROFILE_EVENTS 7
+
+/*
+ * lbmoe_forward with stage timing (instrumentation; no counterpart in the reference).
+ * events[0..6] are caller-created hipEvent_t handles (passed as void*), recorded on `stream`
+ * before the first kernel and after each stage: router logits, top-k routing, permutation,
+ * gate_up + SiLU*mul, down projection, combine. hipEventElapsedTime between consecutive
+ * events gives each stage's device time.
+ */
+int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
+                               void* workspace, size_t workspace_bytes, void* stream,
+                               void* const* events, int32_t n_events);
+
 /*
  * Router logits: the F.linear of Qwen3_5TopKRouter.forward (qwen3_5.py:769).
  * x bf16 [T,H] -> logits bf16 [T,E] (fp32 accumulation, round-to-nearest-even).

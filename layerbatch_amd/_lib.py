@@ -12,6 +12,8 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblbmoe.so")
 
+LBMOE_PROFILE_EVENTS = 7
+PROFILE_STAGES = ("router_logits", "route_topk", "permute", "gate_up", "down", "combine")
 LBMOE_W_BF16 = 0
 LBMOE_W_FP8_E4M3 = 1
 
@@ -48,6 +50,7 @@ _SIGS = {
     "lbmoe_workspace_size": (_i32, [_PL, _i64, ctypes.POINTER(_sz)]),
     "lbmoe_workspace_region": (_i32, [_PL, _i64, _i32, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "lbmoe_forward": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p]),
+    "lbmoe_forward_profiled": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p, ctypes.POINTER(_p), _i32]),
     "lbmoe_router_logits": (_i32, [_PL, _p, _i64, _p, _p]),
     "lbmoe_route": (_i32, [_PL, _p, _p, _i64, _p, _i32, _p, _p, _p]),
     "lbmoe_permute_workspace_size": (_i32, [_i64, _i32, _i32, ctypes.POINTER(_sz)]),

@@ -18,7 +18,7 @@ LIB = os.path.join(PKG, "liblbmoe.so")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++20", "-Wall",
     "-Wno-unused-function", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

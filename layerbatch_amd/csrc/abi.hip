@@ -144,9 +144,24 @@ static P* at(void* ws, const WsLayout& w, int r) {
   } while (0)
 
 // Routed experts of one call: permute, gate_up, down, combine.
+// Optional instrumentation: when ev is non-null, ev->mark(s) records the next event after
+// each stage.
+struct StageEvents {
+  void* const* events;
+  int n;
+  int next;
+  hipError_t mark(hipStream_t s) {
+    if (!events || next >= n) return hipSuccess;
+    return hipEventRecord(static_cast<hipEvent_t>(events[next++]), s);
+  }
+};
+
 static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx, int idx_bytes,
                            const void* topw, const float* sgate, int64_t T, void* y, void* ws,
-                           const WsLayout& w, bool with_shared, hipStream_t s) {
+                           const WsLayout& w, bool with_shared, hipStream_t s,
+                           StageEvents* ev = nullptr) {
+  StageEvents none{nullptr, 0, 0};
+  if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
   const int Imax = std::max(L.moe_intermediate_size, L.shared_intermediate_size);
   int32_t* counts = at<int32_t>(ws, w, R_COUNTS);
@@ -156,13 +171,17 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
                            at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
                            at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
+  LBMOE_TRY(ev->mark(s));
   const GroupWeights gw = group_weights(L, with_shared, T);
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
   if (is_fp8(L)) return LBMOE_ERR_DTYPE;
-  LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, Imax, act, s));
-  LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, out, s));
+  LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
+  LBMOE_TRY(ev->mark(s));
+  LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, k, out, s));
+  LBMOE_TRY(ev->mark(s));
   LBMOE_TRY(launch_combine(out, inv, topw, sgate, T, k, H, with_shared, y, s));
+  LBMOE_TRY(ev->mark(s));
   return LBMOE_OK;
 }
 
@@ -219,8 +238,13 @@ int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t regi
   return LBMOE_OK;
 }
 
-int32_t lbmoe_forward(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace lbmoe {
+
+static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
+                            void* workspace, size_t workspace_bytes, void* stream,
+                            StageEvents* ev) {
   int32_t st = lbmoe_check_layer(layer);
   if (st != LBMOE_OK) return st;
   const lbmoe_layer& L = *layer;
@@ -237,10 +261,31 @@ int32_t lbmoe_forward(const lbmoe_layer* layer, const void* x, int64_t T, void* 
   void* idx = at<void>(ws, w, R_IDX);
   void* topw = at<void>(ws, w, R_TOPW);
   float* sgate = sh ? at<float>(ws, w, R_SGATE) : nullptr;
+  LBMOE_TRY(ev->mark(s));
   LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
+  LBMOE_TRY(ev->mark(s));
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,
                               L.hidden_size, L.top_k, idx, 4, topw, sgate, s));
-  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s);
+  LBMOE_TRY(ev->mark(s));
+  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev);
+}
+
+}  // namespace lbmoe
+
+extern "C" {
+
+int32_t lbmoe_forward(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  StageEvents none{nullptr, 0, 0};
+  return forward_impl(layer, x, T, y, workspace, workspace_bytes, stream, &none);
+}
+
+int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
+                               void* workspace, size_t workspace_bytes, void* stream,
+                               void* const* events, int32_t n_events) {
+  if (!events || n_events < LBMOE_PROFILE_EVENTS) return LBMOE_ERR_NULL;
+  StageEvents ev{events, n_events, 0};
+  return forward_impl(layer, x, T, y, workspace, workspace_bytes, stream, &ev);
 }
 
 int32_t lbmoe_router_logits(const lbmoe_layer* layer, const void* x, int64_t T, void* logits,
@@ -384,8 +429,8 @@ int32_t lbmoe_dense_mlp(const void* gate_proj, const void* up_proj, const void* 
   gw.groups = 1;
   gw.sh_row0 = 0;
   void* act = at<void>(workspace, w, R_ACT);
-  LBMOE_TRY(launch_gate_up_bf16(gw, x, nullptr, nullptr, nullptr, T, Is, act, s));
-  LBMOE_TRY(launch_down_bf16(gw, act, Is, nullptr, nullptr, T, out, s));
+  LBMOE_TRY(launch_gate_up_bf16(gw, x, nullptr, nullptr, nullptr, T, 1, Is, act, s));
+  LBMOE_TRY(launch_down_bf16(gw, act, Is, nullptr, nullptr, T, 1, out, s));
   return LBMOE_OK;
 }
 

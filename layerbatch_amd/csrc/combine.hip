@@ -11,6 +11,10 @@
 
 namespace lbmoe {
 
+// One workgroup per token. The token's k (row, weight) pairs are read first, then every
+// thread issues its k row loads together before accumulating, so the loads overlap.
+constexpr int kCombineSlots = 8;   // slots whose row loads are in flight together
+
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
                                                       const int32_t* __restrict__ inv,
                                                       const uint16_t* __restrict__ topw,
@@ -18,32 +22,41 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
                                                       int k, int H, int sh_row0,
                                                       uint16_t* __restrict__ y) {
   const int t = blockIdx.x;
+  const int32_t* inv_t = inv + static_cast<int64_t>(t) * k;
+  const uint16_t* w_t = topw + static_cast<int64_t>(t) * k;
   for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < k; ++s) {
-      const int64_t ts = static_cast<int64_t>(t) * k + s;
-      const int p = inv[ts];
-      if (p < 0) continue;
-      const float w = bf2f(topw[ts]);
-      const u32x4 o = ld16(rows + static_cast<int64_t>(p) * H + c);
+    for (int s0 = 0; s0 < k; s0 += kCombineSlots) {
+      u32x4 o[kCombineSlots];
+      float w[kCombineSlots];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += w * bf_lo(o[i]);
-        acc[2 * i + 1] += w * bf_hi(o[i]);
+      for (int i = 0; i < kCombineSlots; ++i) {
+        const int s = s0 + i;
+        const int p = s < k ? inv_t[s] : -1;
+        w[i] = p >= 0 ? bf2f(w_t[s]) : 0.f;
+        o[i] = p >= 0 ? ld16(rows + static_cast<int64_t>(p) * H + c) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < kCombineSlots; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += w[i] * bf_lo(o[i][q]);
+          acc[2 * q + 1] += w[i] * bf_hi(o[i][q]);
+        }
       }
     }
     if (sgate != nullptr) {
       const float g = sgate[t];
       const u32x4 o = ld16(rows + static_cast<int64_t>(sh_row0 + t) * H + c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += g * bf_lo(o[i]);
-        acc[2 * i + 1] += g * bf_hi(o[i]);
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] += g * bf_lo(o[q]);
+        acc[2 * q + 1] += g * bf_hi(o[q]);
       }
     }
     u32x4 pk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pk[i] = pack_bf2(acc[2 * i], acc[2 * i + 1]);
+    for (int q = 0; q < 4; ++q) pk[q] = pack_bf2(acc[2 * q], acc[2 * q + 1]);
     *reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + c) = pk;
   }
 }

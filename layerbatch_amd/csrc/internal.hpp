@@ -66,9 +66,9 @@ hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int 
                           int32_t* hist, int32_t* base, int32_t* lrank, hipStream_t s);
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
-                               int act_ld, void* act, hipStream_t s);
+                               int k, int act_ld, void* act, hipStream_t s);
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
-                            const int32_t* counts, const int32_t* offsets, int64_t T,
+                            const int32_t* counts, const int32_t* offsets, int64_t T, int k,
                             void* out, hipStream_t s);
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,

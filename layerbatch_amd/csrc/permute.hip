@@ -36,6 +36,7 @@ __device__ __forceinline__ uint64_t match_expert(int e, uint64_t m, int nbits) {
 }
 
 // Ranks one chunk's entries. Returns per-lane (expert, rank) for round r in e_out/rk_out.
+// All expert ids of the chunk are loaded before the ranking so the loads overlap.
 template <int IB, int ROUNDS>
 __device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E, int nbits,
                                            int V, int v0, int* run, int (&e_out)[ROUNDS],
@@ -50,6 +51,11 @@ __device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E,
       const int t = v - s * T;
       e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
     }
+    e_out[r] = e;
+  }
+#pragma unroll
+  for (int r = 0; r < ROUNDS; ++r) {
+    const int e = e_out[r];
     const bool valid = (e >= 0) && (e < E);
     const uint64_t m = match_expert(valid ? e : 0, __ballot(valid), nbits);
     int rank = -1;

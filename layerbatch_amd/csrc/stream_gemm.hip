@@ -3,8 +3,9 @@
 // Every GEMM of the layer has the form C[rows of W, tokens] = W[rows, K] . X[tokens, K]^T
 // with both operands K-contiguous (the reference's nn.Linear / 3-D expert layouts,
 // nanovllm/models/qwen3_5.py:765, :795-800, :912-914). A wave owns 16*RA weight rows and
-// streams them from HBM exactly once per pass over its group's tokens; the tokens (16 per
-// MFMA column tile, TT tiles per pass) are read through L2.
+// streams them from HBM once per pass over its group's tokens; the tokens (16 per MFMA
+// column tile, TT tiles per pass) are read through L2. This is the decode-sized regime,
+// where the layer is bound by streaming each hit expert's weights once.
 //
 // MFMA operand mapping. For v_mfma_f32_16x16x32_bf16 lane l = 16*q + r supplies row r of A
 // and column r of B, 8 consecutive k each. K is walked in blocks of 128: in block kb lane
@@ -12,12 +13,20 @@
 // of its token row, and MFMA c (c = 0..3) consumes the c-th 8-element chunk. A and B use the
 // same (lane, chunk) -> k map, so the products pair correctly and each weight row is read
 // as 256-byte contiguous segments. Accumulator lane (r, q) holds rows 4q..4q+3 of column r.
+//
+// Loads run kPD k-blocks ahead of the MFMAs. When K/128 is one of the unrolled sizes the
+// whole K loop is unrolled so that the load of block i+kPD and the MFMAs of block i are
+// statically scheduled; other sizes use a rolled loop with one block of lookahead.
 #include "common.hpp"
 #include "internal.hpp"
 
 namespace lbmoe {
 
 constexpr int kKBlock = 128;
+#ifndef LBMOE_STREAM_PD
+#define LBMOE_STREAM_PD 2
+#endif
+constexpr int kPD = LBMOE_STREAM_PD;   // k-blocks of loads in flight ahead of the MFMAs
 
 template <int RA, int TT>
 __device__ __forceinline__ void load_kblock(const uint16_t* const (&arow)[RA],
@@ -35,8 +44,36 @@ __device__ __forceinline__ void load_kblock(const uint16_t* const (&arow)[RA],
       b[j][c] = brow[j] ? ld16(brow[j] + k0 + 8 * c) : u32x4{0, 0, 0, 0};
 }
 
-// acc[i][j] += W-tile i . X-tile j over K (K a multiple of 128). arow/brow are this lane's
-// row pointers (nullptr = zero row), already offset by 32*q.
+template <int RA, int TT>
+__device__ __forceinline__ void mma_kblock(const u32x4 (&a)[RA][4], const u32x4 (&b)[TT][4],
+                                           f32x4 (&acc)[RA][TT]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i][c]), as_bf16x8(b[j][c]),
+                                                            acc[i][j], 0, 0, 0);
+}
+
+// acc[i][j] += W-tile i . X-tile j over NKB k-blocks (fully unrolled, kPD blocks in flight).
+// arow/brow are this lane's row pointers (nullptr = zero row), already offset by 32*q.
+template <int RA, int TT, int NKB>
+__device__ __forceinline__ void stream_mma_fixed(const uint16_t* const (&arow)[RA],
+                                                 const uint16_t* const (&brow)[TT],
+                                                 f32x4 (&acc)[RA][TT]) {
+  u32x4 a[NKB][RA][4], b[NKB][TT][4];
+#pragma unroll
+  for (int p = 0; p < kPD && p < NKB; ++p) load_kblock<RA, TT>(arow, brow, p * kKBlock, a[p], b[p]);
+#pragma unroll
+  for (int i = 0; i < NKB; ++i) {
+    if (i + kPD < NKB) load_kblock<RA, TT>(arow, brow, (i + kPD) * kKBlock, a[i + kPD], b[i + kPD]);
+    mma_kblock<RA, TT>(a[i], b[i], acc);
+  }
+}
+
+// Rolled variant for any K (multiple of 128), one block of lookahead.
 template <int RA, int TT>
 __device__ __forceinline__ void stream_mma(const uint16_t* const (&arow)[RA],
                                            const uint16_t* const (&brow)[TT], int K,
@@ -45,15 +82,7 @@ __device__ __forceinline__ void stream_mma(const uint16_t* const (&arow)[RA],
   load_kblock<RA, TT>(arow, brow, 0, a, b);
   for (int kb = 0; kb < K; kb += kKBlock) {
     if (kb + kKBlock < K) load_kblock<RA, TT>(arow, brow, kb + kKBlock, an, bn);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int i = 0; i < RA; ++i)
-#pragma unroll
-        for (int j = 0; j < TT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i][c]),
-                                                              as_bf16x8(b[j][c]), acc[i][j],
-                                                              0, 0, 0);
+    mma_kblock<RA, TT>(a, b, acc);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -64,6 +93,15 @@ __device__ __forceinline__ void stream_mma(const uint16_t* const (&arow)[RA],
   }
 }
 
+// NKB = 0 selects the rolled loop over K.
+template <int RA, int TT, int NKB>
+__device__ __forceinline__ void stream_dot(const uint16_t* const (&arow)[RA],
+                                           const uint16_t* const (&brow)[TT], int K,
+                                           f32x4 (&acc)[RA][TT]) {
+  if constexpr (NKB > 0) stream_mma_fixed<RA, TT, NKB>(arow, brow, acc);
+  else stream_mma<RA, TT>(arow, brow, K, acc);
+}
+
 template <int RA, int TT>
 __device__ __forceinline__ void zero_acc(f32x4 (&acc)[RA][TT]) {
 #pragma unroll
@@ -72,55 +110,165 @@ __device__ __forceinline__ void zero_acc(f32x4 (&acc)[RA][TT]) {
     for (int j = 0; j < TT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
-// ---- router logits: logits[t, e] = bf16(x[t] . Wg[e]) ----------------------------------
-constexpr int kRouterTT = 2;
+// ---- wide loads + per-wave LDS transpose ---------------------------------------------------
+// HBM streams best when each load instruction covers few rows with long contiguous runs. Here
+// one instruction loads 4 rows x 256 contiguous bytes (16 lanes per row, 16 bytes each): lane l
+// holds row 4u + l/16 (u = instruction), chunk l%16 of the row's 128-element k-block. The MFMA
+// needs row r in lane r (mod 16), so each wave writes its k-block to a private LDS scratch and
+// reads it back transposed. Chunk j of scratch row R sits at slot 16R + (j ^ (R & 15)), which
+// keeps both the 16-lane row writes and the 16-row column reads free of bank conflicts.
+// MFMA c of a k-block consumes chunks 4c..4c+3: lane (r, q) gets chunk 4c + q of row r, i.e.
+// k = kb + 32c + 8q .. +8 for both operands.
+template <int RA, int TT>
+__device__ __forceinline__ void wide_load(const uint16_t* const (&ap)[RA][4],
+                                          const uint16_t* const (&bp)[TT][4], int k0,
+                                          u32x4 (&a)[RA][4], u32x4 (&b)[TT][4]) {
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[i][u] = ap[i][u] ? ld16_stream(ap[i][u] + k0) : u32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < TT; ++j)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[j][u] = bp[j][u] ? ld16(bp[j][u] + k0) : u32x4{0, 0, 0, 0};
+}
 
-__global__ __launch_bounds__(64) void router_logits_kernel(const uint16_t* __restrict__ x,
-                                                           const uint16_t* __restrict__ wg,
-                                                           int T, int E, int H,
-                                                           uint16_t* __restrict__ logits) {
-  const int lane = lane_id(), r = lane & 15, q = lane >> 4;
-  const int e0 = blockIdx.x * 16;
-  const int t0 = blockIdx.y * 16 * kRouterTT;
-  const uint16_t* arow[1] = {e0 + r < E ? wg + static_cast<int64_t>(e0 + r) * H + 32 * q
-                                        : nullptr};
-  const uint16_t* brow[kRouterTT];
+template <int RA, int TT>
+__device__ __forceinline__ void wide_mma(u32x4* __restrict__ lds, const u32x4 (&a)[RA][4],
+                                         const u32x4 (&b)[TT][4], f32x4 (&acc)[RA][TT]) {
+  const int l = lane_id(), r = l & 15, q = l >> 4;
 #pragma unroll
-  for (int j = 0; j < kRouterTT; ++j) {
-    const int t = t0 + 16 * j + r;
-    brow[j] = t < T ? x + static_cast<int64_t>(t) * H + 32 * q : nullptr;
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lds[(16 * i + 4 * u + q) * 16 + (r ^ (4 * u + q))] = a[i][u];
+#pragma unroll
+  for (int j = 0; j < TT; ++j)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lds[(16 * (RA + j) + 4 * u + q) * 16 + (r ^ (4 * u + q))] = b[j][u];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int sl = (4 * c + q) ^ r;
+    u32x4 fa[RA], fb[TT];
+#pragma unroll
+    for (int i = 0; i < RA; ++i) fa[i] = lds[(16 * i + r) * 16 + sl];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) fb[j] = lds[(16 * (RA + j) + r) * 16 + sl];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[i]), as_bf16x8(fb[j]),
+                                                            acc[i][j], 0, 0, 0);
   }
-  f32x4 acc[1][kRouterTT];
-  zero_acc(acc);
-  stream_mma<1, kRouterTT>(arow, brow, H, acc);
+}
+
+// acc += A . B^T over NKB k-blocks, kPD blocks of loads in flight (NKB = 0: rolled loop over K
+// with one block of lookahead). ap/bp are this lane's row pointers (nullptr = zero row),
+// already offset by its 16-byte chunk.
+template <int RA, int TT, int NKB>
+__device__ __forceinline__ void wide_dot(u32x4* __restrict__ lds, const uint16_t* const (&ap)[RA][4],
+                                         const uint16_t* const (&bp)[TT][4], int K,
+                                         f32x4 (&acc)[RA][TT]) {
+  if constexpr (NKB > 0) {
+    u32x4 a[NKB][RA][4], b[NKB][TT][4];
 #pragma unroll
-  for (int j = 0; j < kRouterTT; ++j) {
-    const int t = t0 + 16 * j + r;
-    if (t >= T) continue;
+    for (int p = 0; p < kPD && p < NKB; ++p) wide_load<RA, TT>(ap, bp, p * kKBlock, a[p], b[p]);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int e = e0 + 4 * q + v;
-      if (e < E) logits[static_cast<int64_t>(t) * E + e] = static_cast<uint16_t>(f2bf(acc[0][j][v]));
+    for (int i = 0; i < NKB; ++i) {
+      if (i + kPD < NKB) wide_load<RA, TT>(ap, bp, (i + kPD) * kKBlock, a[i + kPD], b[i + kPD]);
+      wide_mma<RA, TT>(lds, a[i], b[i], acc);
     }
+  } else {
+    u32x4 a[RA][4], b[TT][4], an[RA][4], bn[TT][4];
+    wide_load<RA, TT>(ap, bp, 0, a, b);
+    for (int kb = 0; kb < K; kb += kKBlock) {
+      if (kb + kKBlock < K) wide_load<RA, TT>(ap, bp, kb + kKBlock, an, bn);
+      wide_mma<RA, TT>(lds, a, b, acc);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int i = 0; i < RA; ++i) a[i][u] = an[i][u];
+#pragma unroll
+        for (int j = 0; j < TT; ++j) b[j][u] = bn[j][u];
+      }
+    }
+  }
+}
+
+// Calls f.template operator()<NKB>() with NKB = K/128 when that size is unrolled, else 0.
+template <typename F>
+static hipError_t with_nkb(int K, F&& f) {
+  switch (K / kKBlock) {
+    case 1: return f.template operator()<1>();
+    case 2: return f.template operator()<2>();
+    case 3: return f.template operator()<3>();
+    case 4: return f.template operator()<4>();
+    case 6: return f.template operator()<6>();
+    case 8: return f.template operator()<8>();
+    case 16: return f.template operator()<16>();
+    default: return f.template operator()<0>();
+  }
+}
+
+// ---- router logits: logits[t, e] = bf16(x[t] . Wg[e]) ----------------------------------
+// Workgroup = 4 waves on one 16-expert x 16-token tile, each wave a quarter of K; the four
+// partial sums are added in LDS (fixed order) and rounded once.
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ wg,
+                                                            int T, int E, int H,
+                                                            uint16_t* __restrict__ logits) {
+  __shared__ f32x4 part[3][64];
+  const int lane = lane_id(), r = lane & 15, q = lane >> 4, w = threadIdx.x >> 6;
+  const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+  const int nkb = H / kKBlock;
+  const int kb0 = (nkb * w) / 4, kb1 = (nkb * (w + 1)) / 4;
+  f32x4 acc[1][1];
+  zero_acc(acc);
+  if (kb1 > kb0) {
+    const int koff = kb0 * kKBlock + 32 * q;
+    const uint16_t* arow[1] = {e0 + r < E ? wg + static_cast<int64_t>(e0 + r) * H + koff : nullptr};
+    const uint16_t* brow[1] = {t0 + r < T ? x + static_cast<int64_t>(t0 + r) * H + koff : nullptr};
+    stream_mma<1, 1>(arow, brow, (kb1 - kb0) * kKBlock, acc);
+  }
+  if (w > 0) part[w - 1][lane] = acc[0][0];
+  __syncthreads();
+  if (w != 0) return;
+  f32x4 s = acc[0][0];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) s += part[i][lane];
+  const int t = t0 + r;
+  if (t >= T) return;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int e = e0 + 4 * q + v;
+    if (e < E) logits[static_cast<int64_t>(t) * E + e] = static_cast<uint16_t>(f2bf(s[v]));
   }
 }
 
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
                                 void* logits, hipStream_t s) {
-  const dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 16 * kRouterTT - 1) / (16 * kRouterTT)));
-  router_logits_kernel<<<grid, 64, 0, s>>>(static_cast<const uint16_t*>(x),
-                                           static_cast<const uint16_t*>(wg),
-                                           static_cast<int>(T), E, H,
-                                           static_cast<uint16_t*>(logits));
+  const dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
+  router_logits_kernel<<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x),
+                                            static_cast<const uint16_t*>(wg),
+                                            static_cast<int>(T), E, H,
+                                            static_cast<uint16_t*>(logits));
   return hipGetLastError();
+}
+
+// Token tiles per pass from the expected tokens per routed expert (T*k/E): enough columns
+// that a typical expert's weights stream once, few enough to keep occupancy.
+static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
+  const double avg = gw.g0 < gw.E ? static_cast<double>(T) * k / gw.E : static_cast<double>(T);
+  if (avg <= 12.0) return 1;
+  if (avg <= 28.0) return 2;
+  return 4;
 }
 
 // ---- gate_up + SiLU*mul ------------------------------------------------------------------
 // Wave (channel block cb, group g): gate rows [16cb, 16cb+16) and the matching up rows of
 // expert g; act[row, 16cb + c] = bf16(silu(gate) * up) (chunk(2,-1) + silu*mul of
 // qwen3_5.py:835-836).
-constexpr int kGateUpTT = 2;
-
+template <int TT, int NKB>
 __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
                                                           const uint16_t* __restrict__ x,
                                                           const int32_t* __restrict__ counts,
@@ -147,21 +295,29 @@ __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
     wgt = static_cast<const uint16_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
     wup = wgt + static_cast<int64_t>(gw.I) * H;
   }
-  const uint16_t* arow[2] = {wgt + static_cast<int64_t>(c0 + r) * H + 32 * q,
-                             wup + static_cast<int64_t>(c0 + r) * H + 32 * q};
-  for (int p0 = 0; p0 < n; p0 += 16 * kGateUpTT) {
-    const uint16_t* brow[kGateUpTT];
+  __shared__ u32x4 lds[(2 + TT) * 256];
+  // wide-load row pointers: instruction u covers rows 4u .. 4u+3 of each 16-row tile
+  const uint16_t* ap[2][4];
 #pragma unroll
-    for (int j = 0; j < kGateUpTT; ++j) {
-      const int p = p0 + 16 * j + r;
-      const int tok = p < n ? (shared ? p : perm_tok[row0 + p]) : -1;
-      brow[j] = tok >= 0 ? x + static_cast<int64_t>(tok) * H + 32 * q : nullptr;
-    }
-    f32x4 acc[2][kGateUpTT];
+  for (int u = 0; u < 4; ++u) {
+    ap[0][u] = wgt + static_cast<int64_t>(c0 + 4 * u + q) * H + 8 * r;
+    ap[1][u] = wup + static_cast<int64_t>(c0 + 4 * u + q) * H + 8 * r;
+  }
+  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+    const uint16_t* bp[TT][4];
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + 16 * j + 4 * u + q;
+        const int tok = p < n ? (shared ? p : perm_tok[row0 + p]) : -1;
+        bp[j][u] = tok >= 0 ? x + static_cast<int64_t>(tok) * H + 8 * r : nullptr;
+      }
+    f32x4 acc[2][TT];
     zero_acc(acc);
-    stream_mma<2, kGateUpTT>(arow, brow, H, acc);
+    wide_dot<2, TT, NKB>(lds, ap, bp, H, acc);
 #pragma unroll
-    for (int j = 0; j < kGateUpTT; ++j) {
+    for (int j = 0; j < TT; ++j) {
       const int p = p0 + 16 * j + r;
       if (p >= n) continue;
       float a[4];
@@ -173,32 +329,45 @@ __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
   }
 }
 
+template <int TT>
+static hipError_t launch_gate_up_tt(const GroupWeights& gw, const void* x, const int32_t* counts,
+                                    const int32_t* offsets, const int32_t* perm_tok, int64_t T,
+                                    int act_ld, void* act, hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const dim3 grid(Imax / 16, gw.groups);
+  return with_nkb(gw.H, [&]<int NKB>() {
+    gate_up_bf16_kernel<TT, NKB><<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(x), counts,
+                                                     offsets, perm_tok, static_cast<int>(T),
+                                                     act_ld, static_cast<uint16_t*>(act));
+    return hipGetLastError();
+  });
+}
 
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
-                               int act_ld, void* act, hipStream_t s) {
-  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const dim3 grid(Imax / 16, gw.groups);
-  gate_up_bf16_kernel<<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(x), counts, offsets,
-                                          perm_tok, static_cast<int>(T), act_ld,
-                                          static_cast<uint16_t*>(act));
-  return hipGetLastError();
+                               int k, int act_ld, void* act, hipStream_t s) {
+  switch (pick_tt(gw, T, k)) {
+    case 1: return launch_gate_up_tt<1>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
+    case 2: return launch_gate_up_tt<2>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
+    default: return launch_gate_up_tt<4>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
+  }
 }
 
 // ---- down projection ---------------------------------------------------------------------
 // Wave (row block hb, group g): output columns [32hb, 32hb+32) of H for every token row of the
 // group: out[row, h] = bf16(act[row, :Ig] . Wd_g[h, :Ig]) (qwen3_5.py:837, :868, :917).
-constexpr int kDownTT = 2;
-
+template <int TT, int NKB>
 __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
                                                        const uint16_t* __restrict__ act,
                                                        int act_ld,
                                                        const int32_t* __restrict__ counts,
                                                        const int32_t* __restrict__ offsets,
-                                                       int T, uint16_t* __restrict__ out) {
+                                                       int T, int width,
+                                                       uint16_t* __restrict__ out) {
   const int g = gw.g0 + blockIdx.y;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
+  if (Ig != width) return;          // groups of another width run in their own launch
   const int n = shared ? T : counts[g];
   if (n == 0) return;
   const int row0 = shared ? gw.sh_row0 : offsets[g];
@@ -208,20 +377,27 @@ __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
   const uint16_t* wd = shared ? static_cast<const uint16_t*>(gw.sh_down)
                               : static_cast<const uint16_t*>(gw.down) +
                                     static_cast<int64_t>(g) * H * gw.I;
-  const uint16_t* arow[2] = {wd + static_cast<int64_t>(h0 + r) * Ig + 32 * q,
-                             wd + static_cast<int64_t>(h0 + 16 + r) * Ig + 32 * q};
-  for (int p0 = 0; p0 < n; p0 += 16 * kDownTT) {
-    const uint16_t* brow[kDownTT];
+  __shared__ u32x4 lds[(2 + TT) * 256];
+  const uint16_t* ap[2][4];
 #pragma unroll
-    for (int j = 0; j < kDownTT; ++j) {
-      const int p = p0 + 16 * j + r;
-      brow[j] = p < n ? act + static_cast<int64_t>(row0 + p) * act_ld + 32 * q : nullptr;
-    }
-    f32x4 acc[2][kDownTT];
+  for (int u = 0; u < 4; ++u) {
+    ap[0][u] = wd + static_cast<int64_t>(h0 + 4 * u + q) * Ig + 8 * r;
+    ap[1][u] = wd + static_cast<int64_t>(h0 + 16 + 4 * u + q) * Ig + 8 * r;
+  }
+  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+    const uint16_t* bp[TT][4];
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + 16 * j + 4 * u + q;
+        bp[j][u] = p < n ? act + static_cast<int64_t>(row0 + p) * act_ld + 8 * r : nullptr;
+      }
+    f32x4 acc[2][TT];
     zero_acc(acc);
-    stream_mma<2, kDownTT>(arow, brow, Ig, acc);
+    wide_dot<2, TT, NKB>(lds, ap, bp, Ig, acc);
 #pragma unroll
-    for (int j = 0; j < kDownTT; ++j) {
+    for (int j = 0; j < TT; ++j) {
       const int p = p0 + 16 * j + r;
       if (p >= n) continue;
       uint16_t* orow = out + static_cast<int64_t>(row0 + p) * H + h0 + 4 * q;
@@ -234,14 +410,37 @@ __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
   }
 }
 
-hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
-                            const int32_t* counts, const int32_t* offsets, int64_t T,
-                            void* out, hipStream_t s) {
+template <int TT>
+static hipError_t launch_down_tt(const GroupWeights& gw, const void* act, int act_ld,
+                                 const int32_t* counts, const int32_t* offsets, int64_t T,
+                                 void* out, hipStream_t s) {
   const dim3 grid(gw.H / 32, gw.groups);
-  down_bf16_kernel<<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(act), act_ld, counts,
-                                       offsets, static_cast<int>(T),
-                                       static_cast<uint16_t*>(out));
-  return hipGetLastError();
+  auto go = [&](int K) {
+    return with_nkb(K, [&]<int NKB>() {
+      down_bf16_kernel<TT, NKB><<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(act), act_ld,
+                                                    counts, offsets, static_cast<int>(T), K,
+                                                    static_cast<uint16_t*>(out));
+      return hipGetLastError();
+    });
+  };
+  // Routed experts (width I) and the shared expert (width Is) each get the kernel unrolled
+  // for their width; a group whose width differs from the launch's exits at once.
+  const bool has_routed = gw.g0 < gw.E;
+  const bool has_shared = gw.g0 + gw.groups > gw.E;
+  hipError_t e = hipSuccess;
+  if (has_routed) e = go(gw.I);
+  if (e == hipSuccess && has_shared && (!has_routed || gw.Is != gw.I)) e = go(gw.Is);
+  return e;
+}
+
+hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
+                            const int32_t* counts, const int32_t* offsets, int64_t T, int k,
+                            void* out, hipStream_t s) {
+  switch (pick_tt(gw, T, k)) {
+    case 1: return launch_down_tt<1>(gw, act, act_ld, counts, offsets, T, out, s);
+    case 2: return launch_down_tt<2>(gw, act, act_ld, counts, offsets, T, out, s);
+    default: return launch_down_tt<4>(gw, act, act_ld, counts, offsets, T, out, s);
+  }
 }
 
 }  // namespace lbmoe
