@@ -35,6 +35,7 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
   w.bytes[R_HIST] = E * nblk * 4;
   w.bytes[R_BASE] = E * nblk * 4;
   w.bytes[R_LRANK] = V * 4;
+  w.bytes[R_TILES] = (2 * static_cast<int64_t>(tiled_max_tiles(Vs, E + 1)) + 1) * 4;
   if (is_fp8(L)) {
     w.bytes[R_XQ] = T * H;
     w.bytes[R_XS] = T * (H / 128) * 4;
@@ -143,6 +144,13 @@ static P* at(void* ws, const WsLayout& w, int r) {
     if ((expr) != hipSuccess) return LBMOE_ERR_LAUNCH;        \
   } while (0)
 
+// Expected tokens per routed expert at which the LDS-tiled GEMMs replace weight streaming.
+constexpr double kTiledMinTokensPerExpert = 48.0;
+
+static bool use_tiled(const GroupWeights& gw, int64_t T, int k) {
+  return tiled_supported(gw) && static_cast<double>(T) * k / gw.E >= kTiledMinTokensPerExpert;
+}
+
 // Routed experts of one call: permute, gate_up, down, combine.
 // Optional instrumentation: when ev is non-null, ev->mark(s) records the next event after
 // each stage.
@@ -176,9 +184,20 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
   if (is_fp8(L)) return LBMOE_ERR_DTYPE;
-  LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
-  LBMOE_TRY(ev->mark(s));
-  LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, k, out, s));
+  if (use_tiled(gw, T, k)) {
+    // prefill-sized batch: LDS-tiled MFMA GEMMs over a device-built token-tile list
+    int32_t* tiles = at<int32_t>(ws, w, R_TILES);
+    const int max_tiles = tiled_max_tiles(T * k + (with_shared ? T : 0), gw.groups);
+    LBMOE_TRY(launch_build_tiles(counts, E, with_shared, T, max_tiles, tiles, s));
+    LBMOE_TRY(launch_gate_up_tiled(gw, x, counts, offsets, perm_tok, tiles, max_tiles, T, Imax,
+                                   act, s));
+    LBMOE_TRY(ev->mark(s));
+    LBMOE_TRY(launch_down_tiled(gw, act, Imax, counts, offsets, tiles, max_tiles, T, out, s));
+  } else {
+    LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
+    LBMOE_TRY(ev->mark(s));
+    LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, k, out, s));
+  }
   LBMOE_TRY(ev->mark(s));
   LBMOE_TRY(launch_combine(out, inv, topw, sgate, T, k, H, with_shared, y, s));
   LBMOE_TRY(ev->mark(s));

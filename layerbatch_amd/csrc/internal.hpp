@@ -18,7 +18,7 @@ enum Region {
   R_LOGITS = 0, R_IDX, R_TOPW, R_SGATE, R_COUNTS, R_OFFSETS, R_PERM_TOK, R_PERM_SLOT, R_INV,
   R_ACT, R_OUT,
   // private regions (not exposed through lbmoe_workspace_region)
-  R_HIST, R_BASE, R_LRANK, R_XQ, R_XS, R_ACTQ, R_ACTS,
+  R_HIST, R_BASE, R_LRANK, R_TILES, R_XQ, R_XS, R_ACTQ, R_ACTS,
   R_COUNT_
 };
 constexpr int kPublicRegions = R_OUT + 1;
@@ -73,6 +73,18 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,
                           void* y, hipStream_t s);
+// LDS-tiled grouped GEMMs (prefill-sized batches).
+int tiled_max_tiles(int64_t rows, int groups);   // rows = routed + shared rows
+bool tiled_supported(const GroupWeights& gw);
+hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
+                              int32_t* tiles, hipStream_t s);
+hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
+                                const int32_t* offsets, const int32_t* perm_tok,
+                                const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
+                                void* act, hipStream_t s);
+hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
+                             const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
+                             int max_tiles, int64_t T, void* out, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
 hipError_t launch_quant_blocks_fp8(const void* w, int64_t batch, int N, int K, void* q,
                                    float* scale, hipStream_t s);

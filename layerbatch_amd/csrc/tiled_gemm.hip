@@ -1,0 +1,284 @@
+// LDS-tiled grouped GEMMs for prefill-sized batches (gfx950, v_mfma_f32_32x32x16_bf16).
+//
+// Same products as the streaming kernels (gate_up + SiLU*mul, qwen3_5.py:835-836; down,
+// qwen3_5.py:837), for groups with many tokens: a workgroup multiplies a tile of kWM weight
+// rows by a tile of kWT tokens of one expert, staging both operands through LDS in k-tiles of
+// kBK, double buffered, so each operand byte fetched from L2 feeds kWT (or kWM) MFMA columns.
+//
+// Work list. build_tiles turns the per-expert token counts into a list of (group, first row)
+// token tiles; a launch covers max_tiles x n_tiles workgroups (a function of T only) and
+// workgroups past the list's end exit. Consecutive workgroups of one XCD take consecutive
+// (token tile, weight tile) pairs, weight tile fastest, so the tiles that share a token tile
+// run together on one XCD's L2.
+//
+// Layout. A = weight rows (MFMA rows), B = tokens (MFMA columns). Accumulator lane l of a
+// 32x32 tile holds token column l%32 and weight rows 8(v/4) + 4(l/32) + v%4, v = 0..15, so
+// four consecutive output channels of one token are stored together. LDS rows are kBK bf16
+// (128 bytes) in 16-byte chunks; chunk j of row r is stored at chunk j ^ ((r >> 1) & 7), which
+// keeps the 8-lane row writes and the 32-row MFMA operand reads free of bank conflicts.
+// Gate_up workgroups take kWM/2 channels: wave row-half h holds gate rows then up rows of the
+// same kWM/4 channels, so SiLU*mul pairs accumulators in registers.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace lbmoe {
+
+constexpr int kWM = 256;            // weight rows per workgroup
+constexpr int kWT = 128;            // tokens per workgroup
+constexpr int kBK = 64;             // k per LDS stage
+constexpr int kChunks = kBK / 8;    // 16-byte chunks per LDS row
+constexpr int kMT = kWM / 2 / 32;   // 32-row MFMA tiles per wave (weights)
+constexpr int kNT = kWT / 2 / 32;   // 32-column MFMA tiles per wave (tokens)
+constexpr int kALoads = kWM * kChunks / 256;   // 16-byte loads per thread per stage
+constexpr int kBLoads = kWT * kChunks / 256;
+
+__device__ __forceinline__ int swz(int r, int j) { return r * kChunks + (j ^ ((r >> 1) & 7)); }
+
+// ---- tile list -------------------------------------------------------------------------------
+// tiles[2i] = group, tiles[2i+1] = first row within the group, in group order;
+// tiles[2*max_tiles] = number of valid entries. Groups: routed experts 0..E-1 with counts[g]
+// rows, then the shared expert (T rows) when present.
+__global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
+                                                           int E, int shared, int T, int max_tiles,
+                                                           int32_t* __restrict__ tiles) {
+  __shared__ int wsum[16];
+  const int G = E + shared;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (G + 1023) / 1024;
+  const int lo = min(G, tid * per), hi = min(G, lo + per);
+  int local = 0;
+  for (int g = lo; g < hi; ++g) {
+    const int n = g < E ? counts[g] : T;
+    local += (n + kWT - 1) / kWT;
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < 16 ? wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(w, o, kWave);
+      if (lane >= o) w += y;
+    }
+    if (lane < 16) wsum[lane] = w;
+  }
+  __syncthreads();
+  int pos = incl - local + (wave > 0 ? wsum[wave - 1] : 0);
+  for (int g = lo; g < hi; ++g) {
+    const int n = g < E ? counts[g] : T;
+    for (int r = 0; r < n; r += kWT) {
+      if (pos < max_tiles) {
+        tiles[2 * pos] = g;
+        tiles[2 * pos + 1] = r;
+      }
+      ++pos;
+    }
+  }
+  if (tid == 0) tiles[2 * max_tiles] = min(wsum[15], max_tiles);
+}
+
+// ---- the tiled kernel ----------------------------------------------------------------------
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src,
+                                                    int src_ld, const int32_t* __restrict__ offsets,
+                                                    const int32_t* __restrict__ counts,
+                                                    const int32_t* __restrict__ perm_tok,
+                                                    const int32_t* __restrict__ tiles,
+                                                    int max_tiles, int n_wtiles, int T,
+                                                    uint16_t* __restrict__ dst, int dst_ld) {
+  __shared__ u32x4 lds[2][(kWM + kWT) * kChunks];
+  // XCD-aware order: hardware hands out workgroup b to XCD b % 8.
+  const int nblk = gridDim.x;
+  const int b = blockIdx.x;
+  const int per_xcd = nblk / 8;                      // nblk is a multiple of 8
+  const int logical = (b % 8) * per_xcd + b / 8;
+  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
+  if (ti >= tiles[2 * max_tiles]) return;
+  const int g = tiles[2 * ti], r0 = tiles[2 * ti + 1];
+  const bool shared = g == gw.E;
+  const int Ig = shared ? gw.Is : gw.I;
+  const int H = gw.H;
+  const int n = shared ? T : counts[g];
+  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  const int K = GATEUP ? H : Ig;
+  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel (gate_up) / column (down)
+  if (c0 >= (GATEUP ? Ig : H)) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1;
+
+  // Global row pointers of this thread's loads (fixed across k).
+  const uint16_t* wbase;
+  const uint16_t* wup = nullptr;
+  if (GATEUP) {
+    if (shared) {
+      wbase = static_cast<const uint16_t*>(gw.sh_gate);
+      wup = static_cast<const uint16_t*>(gw.sh_up);
+    } else {
+      wbase = static_cast<const uint16_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
+      wup = wbase + static_cast<int64_t>(gw.I) * H;
+    }
+  } else {
+    wbase = shared ? static_cast<const uint16_t*>(gw.sh_down)
+                   : static_cast<const uint16_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
+  }
+  const int jc = tid & 7;                 // chunk within the 128-byte row segment
+  const uint16_t* ap[kALoads];
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) {
+    const int lr = (tid >> 3) + 32 * i;   // local weight row 0..kWM-1
+    int grow;
+    const uint16_t* base = wbase;
+    if (GATEUP) {
+      const int half = lr / (kWM / 2), sub = lr % (kWM / 2);
+      const int ch = c0 + half * (kWM / 4) + (sub % (kWM / 4));
+      base = sub < kWM / 4 ? wbase : wup;
+      grow = ch;
+    } else {
+      grow = c0 + lr;
+    }
+    ap[i] = base + static_cast<int64_t>(grow) * K + 8 * jc;
+  }
+  const uint16_t* bp[kBLoads];
+#pragma unroll
+  for (int i = 0; i < kBLoads; ++i) {
+    const int lt = (tid >> 3) + 32 * i;   // local token 0..kWT-1
+    const int p = r0 + lt;
+    if (p < n) {
+      const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
+      bp[i] = src + static_cast<int64_t>(srow) * src_ld + 8 * jc;
+    } else {
+      bp[i] = nullptr;
+    }
+  }
+
+  f32x16 acc[kMT][kNT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i)
+#pragma unroll
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  u32x4 ra[kALoads], rb[kBLoads];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i) ra[i] = ld16(ap[i] + k0);
+#pragma unroll
+    for (int i = 0; i < kBLoads; ++i) rb[i] = bp[i] ? ld16(bp[i] + k0) : u32x4{0, 0, 0, 0};
+  };
+  auto lstore = [&](u32x4* buf) {
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i) buf[swz((tid >> 3) + 32 * i, jc)] = ra[i];
+#pragma unroll
+    for (int i = 0; i < kBLoads; ++i) buf[swz(kWM + (tid >> 3) + 32 * i, jc)] = rb[i];
+  };
+
+  const int nk = K / kBK;
+  gload(0);
+  lstore(lds[0]);
+  __syncthreads();
+  const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
+  for (int kt = 0; kt < nk; ++kt) {
+    const u32x4* cur = lds[kt & 1];
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int j = 2 * ks + mk;
+      u32x4 fa[kMT], fb[kNT];
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) fa[i] = cur[swz(wm * (kWM / 2) + 32 * i + mr, j)];
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) fb[t] = cur[swz(kWM + wn * (kWT / 2) + 32 * t + mr, j)];
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int t = 0; t < kNT; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa[i]), as_bf16x8(fb[t]),
+                                                              acc[i][t], 0, 0, 0);
+    }
+    if (kt + 1 < nk) lstore(lds[(kt + 1) & 1]);
+    __syncthreads();
+  }
+
+  // Epilogue.
+  const int col = lane & 31, rq = 4 * (lane >> 5);
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) {
+    const int p = r0 + wn * (kWT / 2) + 32 * t + col;
+    if (p >= n) continue;
+    uint16_t* orow = dst + static_cast<int64_t>(row0 + p) * dst_ld;
+    if (GATEUP) {
+#pragma unroll
+      for (int i = 0; i < kMT / 2; ++i)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          float a[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            a[v] = silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v];
+          const int ch = c0 + wm * (kWM / 4) + 32 * i + 8 * v4 + rq;
+          *reinterpret_cast<u32x2*>(orow + ch) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int h = c0 + wm * (kWM / 2) + 32 * i + 8 * v4 + rq;
+          *reinterpret_cast<u32x2*>(orow + h) =
+              u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
+                    pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
+        }
+    }
+  }
+}
+
+// Upper bound of the token-tile count: every group adds at most one partial tile.
+int tiled_max_tiles(int64_t rows, int groups) {
+  return static_cast<int>((rows + kWT - 1) / kWT) + groups + 1;
+}
+
+bool tiled_supported(const GroupWeights& gw) {
+  return gw.H % kWM == 0 && gw.H % kBK == 0 && gw.I % (kWM / 2) == 0 &&
+         (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBK == 0;
+}
+
+hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
+                              int32_t* tiles, hipStream_t s) {
+  build_tiles_kernel<<<1, 1024, 0, s>>>(counts, E, shared ? 1 : 0, static_cast<int>(T), max_tiles,
+                                        tiles);
+  return hipGetLastError();
+}
+
+static unsigned round8(int64_t v) { return static_cast<unsigned>((v + 7) / 8 * 8); }
+
+hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
+                                const int32_t* offsets, const int32_t* perm_tok,
+                                const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
+                                void* act, hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const int n_wtiles = Imax / (kWM / 2);
+  tiled_kernel<true><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), gw.H, offsets, counts, perm_tok, tiles, max_tiles,
+      n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
+  return hipGetLastError();
+}
+
+hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
+                             const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
+                             int max_tiles, int64_t T, void* out, hipStream_t s) {
+  const int n_wtiles = gw.H / kWM;
+  tiled_kernel<false><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
+      gw, static_cast<const uint16_t*>(act), act_ld, offsets, counts, nullptr, tiles, max_tiles,
+      n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
+  return hipGetLastError();
+}
+
+}  // namespace lbmoe

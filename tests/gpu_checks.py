@@ -12,16 +12,18 @@ TOL_BF16 = 1e-2
 TOL_FP8 = 3e-2
 
 
-def check_logits(gpu_bits, x, wg, max_frac=2e-3):
+def check_logits(gpu_bits, x, wg, max_frac=2e-3, acc_tol=2e-5):
     """GPU bf16 logits vs the correctly rounded bf16 of the exact dot products.
 
-    A GPU value may differ from the oracle's only by one bf16 step and only where the exact
-    value lies within fp32-accumulation distance of a rounding midpoint.
+    The GPU accumulates in fp32 in its own order, so its value is bf16(e + d) for the exact
+    dot product e and an accumulation error |d| <= acc_tol * sum_i |x_i w_i|. Every GPU logit
+    must lie in [bf16(e - tol), bf16(e + tol)], and at most max_frac of them may differ from
+    the correctly rounded bf16(e) at all.
     """
     x64 = np.asarray(x, np.float64)
     w64 = np.asarray(wg, np.float64)
     exact = x64 @ w64.T
-    mag = np.abs(x64) @ np.abs(w64).T                       # sum |x_i w_i|
+    tol = acc_tol * (np.abs(x64) @ np.abs(w64).T)
     ref_bits = bf16_bits(exact.astype(np.float32))
     gpu_bits = np.asarray(gpu_bits, np.uint16)
     diff = gpu_bits != ref_bits
@@ -29,14 +31,11 @@ def check_logits(gpu_bits, x, wg, max_frac=2e-3):
     assert frac <= max_frac, f"{frac:.2e} of logits differ from the oracle"
     if diff.any():
         g = bf16_from_bits(gpu_bits[diff]).astype(np.float64)
-        r = bf16_from_bits(ref_bits[diff]).astype(np.float64)
-        e = exact[diff]
-        mid = 0.5 * (g + r)
-        step = np.abs(g - r)
-        # the two candidates must be adjacent bf16 values around the exact result
-        assert np.all(np.abs(g - e) <= step + 1e-30), "GPU logit is not a neighbour of the exact value"
-        slack = 1e-5 * mag[diff] + 1e-30
-        assert np.all(np.abs(e - mid) <= slack), "logit differs away from a rounding midpoint"
+        lo = bf16_round((exact[diff] - tol[diff]).astype(np.float32)).astype(np.float64)
+        hi = bf16_round((exact[diff] + tol[diff]).astype(np.float32)).astype(np.float64)
+        bad = (g < lo) | (g > hi)
+        assert not bad.any(), (f"{int(bad.sum())} logits outside fp32-accumulation reach of the "
+                               f"exact value, e.g. gpu {g[bad][:3]} exact {exact[diff][bad][:3]}")
     return frac
 
 

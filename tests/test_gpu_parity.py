@@ -39,7 +39,7 @@ def _region(blk, ws, T, name, dtype, shape):
     return ws[off:off + n * esz].view(dtype).view(shape)
 
 
-def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu"):
+def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu", sample=None):
     w, g = make_layer(shape, seed=seed, device=gen_device)
     x = make_x(g, T, shape.hidden_size, device=gen_device)
     wd = {k_: v.to(device) for k_, v in w.items()}
@@ -66,9 +66,11 @@ def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu"):
                          to_np(_region(blk, ws, T, "perm_tok", torch.int32, (V,))),
                          to_np(_region(blk, ws, T, "perm_slot", torch.int32, (V,))),
                          to_np(_region(blk, ws, T, "inv", torch.int32, (T, k))))
-    y_ref = gc.block_reference(xn, wn, idx_ref, to_np(topw), k,
+    rows = np.arange(T) if sample is None else np.unique(
+        np.random.default_rng(seed).choice(T, size=min(sample, T), replace=False))
+    y_ref = gc.block_reference(xn[rows], wn, idx_ref[rows], to_np(topw)[rows], k,
                                shared=True if shape.shared_expert_intermediate_size else None)
-    return gc.check_output(to_np(y), y_ref, gc.TOL_BF16)
+    return gc.check_output(to_np(y)[rows], y_ref, gc.TOL_BF16)
 
 
 def test_block_small_layer(gpu):
@@ -90,6 +92,21 @@ def test_block_with_bias(gpu):
     shape = MoEShape(1024, 64, 6, 256, 0)
     g = torch.Generator().manual_seed(11)
     _run_and_check(shape, 200, gpu, seed=5, bias=zipf_bias(g, 64))
+
+
+@pytest.mark.parametrize("T", [3072, 5000])
+def test_block_prefill_tiled_zipf(gpu, T):
+    """Prefill-sized batch (tiled GEMMs) with Zipf-skewed expert loads: empty experts,
+    a hot expert with thousands of tokens, ragged tails."""
+    shape = MoEShape(1024, 32, 4, 256, 0)
+    g = torch.Generator().manual_seed(21)
+    _run_and_check(shape, T, gpu, seed=7, bias=zipf_bias(g, 32), sample=96)
+
+
+def test_block_prefill_tiled_shared(gpu):
+    """Tiled GEMMs with a shared expert of a different width (Is != I)."""
+    shape = MoEShape(512, 16, 2, 256, 384)
+    _run_and_check(shape, 1500, gpu, seed=8, sample=96)
 
 
 def test_dense_reduction_e1_k1(gpu):
