@@ -100,6 +100,10 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
 }
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware reciprocal (v_rcp_f32, about 1 ulp): the result
+// is rounded to bf16 (or quantised to e4m3) right after, far coarser than the rcp error.
+__device__ __forceinline__ float silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 
 }  // namespace lbmoe

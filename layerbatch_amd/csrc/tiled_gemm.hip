@@ -3,7 +3,9 @@
 // Same products as the streaming kernels (gate_up + SiLU*mul, qwen3_5.py:835-836; down,
 // qwen3_5.py:837), for groups with many tokens: a workgroup multiplies a tile of kWM weight
 // rows by a tile of kWT tokens of one expert, staging both operands through LDS in k-tiles of
-// kBK, double buffered, so each operand byte fetched from L2 feeds kWT (or kWM) MFMA columns.
+// kBK, so each operand byte fetched from L2 feeds kWT (or kWM) MFMA columns. The k-tiles move
+// global -> LDS directly (global_load_lds_dwordx4, no register staging) through a ring of
+// kStages buffers, loads running kStages-1 tiles ahead of the MFMAs.
 //
 // Work list. build_tiles turns the per-expert token counts into a list of (group, first row)
 // token tiles; a launch covers max_tiles x n_tiles workgroups (a function of T only) and
@@ -14,8 +16,8 @@
 // Layout. A = weight rows (MFMA rows), B = tokens (MFMA columns). Accumulator lane l of a
 // 32x32 tile holds token column l%32 and weight rows 8(v/4) + 4(l/32) + v%4, v = 0..15, so
 // four consecutive output channels of one token are stored together. LDS rows are kBK bf16
-// (128 bytes) in 16-byte chunks; chunk j of row r is stored at chunk j ^ ((r >> 1) & 7), which
-// keeps the 8-lane row writes and the 32-row MFMA operand reads free of bank conflicts.
+// (64 bytes) in 16-byte chunks; chunk j of row r is stored at chunk j ^ ((r >> 2) & 3), which
+// keeps the 32-row MFMA operand reads free of bank conflicts.
 // Gate_up workgroups take kWM/2 channels: wave row-half h holds gate rows then up rows of the
 // same kWM/4 channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
@@ -23,16 +25,81 @@
 
 namespace lbmoe {
 
-constexpr int kWM = 256;            // weight rows per workgroup
-constexpr int kWT = 128;            // tokens per workgroup
-constexpr int kBK = 64;             // k per LDS stage
-constexpr int kChunks = kBK / 8;    // 16-byte chunks per LDS row
-constexpr int kMT = kWM / 2 / 32;   // 32-row MFMA tiles per wave (weights)
-constexpr int kNT = kWT / 2 / 32;   // 32-column MFMA tiles per wave (tokens)
-constexpr int kALoads = kWM * kChunks / 256;   // 16-byte loads per thread per stage
-constexpr int kBLoads = kWT * kChunks / 256;
+// Tile configuration: kWavesM x kWavesN waves per workgroup, each wave owning kMT x kNT
+// 32x32 MFMA tiles (weights x tokens).
+#ifndef LBMOE_TILE_WAVES_N
+#define LBMOE_TILE_WAVES_N 1
+#endif
+#ifndef LBMOE_TILE_NT
+#define LBMOE_TILE_NT 4
+#endif
+#ifndef LBMOE_TILE_WPE
+#define LBMOE_TILE_WPE 1
+#endif
+constexpr int kWavesM = 2;
+constexpr int kWavesN = LBMOE_TILE_WAVES_N;
+constexpr int kMT = 4;                              // 32-row MFMA tiles per wave (weights)
+constexpr int kNT = LBMOE_TILE_NT;                  // 32-column MFMA tiles per wave (tokens)
+constexpr int kWaves = kWavesM * kWavesN;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kWM = kWavesM * kMT * 32;             // weight rows per workgroup
+constexpr int kWT = kWavesN * kNT * 32;             // tokens per workgroup
+#ifndef LBMOE_TILE_BK
+#define LBMOE_TILE_BK 32
+#endif
+constexpr int kBK = LBMOE_TILE_BK;                  // k per LDS stage
+#ifndef LBMOE_TILE_STAGES
+#define LBMOE_TILE_STAGES 3
+#endif
+constexpr int kStages = LBMOE_TILE_STAGES;          // LDS ring depth
+constexpr int kChunks = kBK / 8;                    // 16-byte chunks per LDS row
+constexpr int kRowsPerLoad = 64 / kChunks;          // rows one wave load covers
+constexpr int kALoads = kWM / kRowsPerLoad / kWaves;   // wave loads per stage (weights)
+constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;   // wave loads per stage (tokens)
+constexpr int kStageU4 = (kWM + kWT) * kChunks;     // 16-byte slots per stage
+static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
+              "loads must tile the stage");
 
-__device__ __forceinline__ int swz(int r, int j) { return r * kChunks + (j ^ ((r >> 1) & 7)); }
+constexpr int kKSteps = kBK / 16;                  // MFMA k-steps per stage
+// Chunk j of LDS row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
+// kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
+constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
+static_assert(kChunks == 4 || kChunks == 8, "kBK must be 32 or 64");
+__device__ __forceinline__ int swz(int r, int j) {
+  return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
+}
+
+// Workgroup barrier for the LDS ring: the wave's LDS reads are complete (lgkmcnt 0) and its
+// own global->LDS copies were waited for by the caller; unlike __syncthreads this does not
+// drain the copies still in flight for later stages. The signal fences keep the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((0x3f & 0xf) | ((0x3f >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Wait until the oldest in-flight stage's copies have landed while the copies of up to
+// min(S, later) younger stages stay in flight (vector-memory ops complete in order).
+template <int S>
+__device__ __forceinline__ void wait_ring(int later) {
+  constexpr int L = kALoads + kBLoads;
+  static_assert(S * L < 64, "vmcnt holds at most 63 outstanding operations");
+  if constexpr (S <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= S) wait_vmcnt<S * L>();
+    else wait_ring<S - 1>(later);
+  }
+}
 
 // ---- tile list -------------------------------------------------------------------------------
 // tiles[2i] = group, tiles[2i+1] = first row within the group, in group order;
@@ -85,14 +152,14 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
 
 // ---- the tiled kernel ----------------------------------------------------------------------
 template <bool GATEUP>
-__global__ __launch_bounds__(256) void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_TILE_WPE, LBMOE_TILE_WPE))) void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src,
                                                     int src_ld, const int32_t* __restrict__ offsets,
                                                     const int32_t* __restrict__ counts,
                                                     const int32_t* __restrict__ perm_tok,
                                                     const int32_t* __restrict__ tiles,
                                                     int max_tiles, int n_wtiles, int T,
                                                     uint16_t* __restrict__ dst, int dst_ld) {
-  __shared__ u32x4 lds[2][(kWM + kWT) * kChunks];
+  __shared__ u32x4 lds[kStages][kStageU4];
   // XCD-aware order: hardware hands out workgroup b to XCD b % 8.
   const int nblk = gridDim.x;
   const int b = blockIdx.x;
@@ -110,10 +177,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(GroupWeights gw, const uint1
   const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel (gate_up) / column (down)
   if (c0 >= (GATEUP ? Ig : H)) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w & 1, wn = w >> 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w % kWavesM, wn = w / kWavesM;
 
-  // Global row pointers of this thread's loads (fixed across k).
+  // Direct global->LDS loads: wave load i writes one contiguous 1 KB LDS block of
+  // kRowsPerLoad rows; lane l fills slot l of it, i.e. row R0 + l/kChunks at swizzled position
+  // l%kChunks, so it fetches the chunk that the swizzle places there.
   const uint16_t* wbase;
   const uint16_t* wup = nullptr;
   if (GATEUP) {
@@ -128,34 +197,32 @@ __global__ __launch_bounds__(256) void tiled_kernel(GroupWeights gw, const uint1
     wbase = shared ? static_cast<const uint16_t*>(gw.sh_down)
                    : static_cast<const uint16_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
   }
-  const int jc = tid & 7;                 // chunk within the 128-byte row segment
+  const int lrow = lane / kChunks, lpos = lane % kChunks;
   const uint16_t* ap[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
-    const int lr = (tid >> 3) + 32 * i;   // local weight row 0..kWM-1
+    const int row = (w * kALoads + i) * kRowsPerLoad + lrow;    // local weight row
+    const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
     int grow;
     const uint16_t* base = wbase;
     if (GATEUP) {
-      const int half = lr / (kWM / 2), sub = lr % (kWM / 2);
-      const int ch = c0 + half * (kWM / 4) + (sub % (kWM / 4));
+      const int half = row / (kWM / 2), sub = row % (kWM / 2);
       base = sub < kWM / 4 ? wbase : wup;
-      grow = ch;
+      grow = c0 + half * (kWM / 4) + (sub % (kWM / 4));
     } else {
-      grow = c0 + lr;
+      grow = c0 + row;
     }
-    ap[i] = base + static_cast<int64_t>(grow) * K + 8 * jc;
+    ap[i] = base + static_cast<int64_t>(grow) * K + 8 * j;
   }
   const uint16_t* bp[kBLoads];
 #pragma unroll
   for (int i = 0; i < kBLoads; ++i) {
-    const int lt = (tid >> 3) + 32 * i;   // local token 0..kWT-1
-    const int p = r0 + lt;
-    if (p < n) {
-      const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
-      bp[i] = src + static_cast<int64_t>(srow) * src_ld + 8 * jc;
-    } else {
-      bp[i] = nullptr;
-    }
+    const int lt = (w * kBLoads + i) * kRowsPerLoad + lrow;     // local token
+    const int row = kWM + lt;
+    const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
+    const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
+    const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
+    bp[i] = src + static_cast<int64_t>(srow) * src_ld + 8 * j;
   }
 
   f32x16 acc[kMT][kNT];
@@ -166,52 +233,71 @@ __global__ __launch_bounds__(256) void tiled_kernel(GroupWeights gw, const uint1
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  u32x4 ra[kALoads], rb[kBLoads];
-  auto gload = [&](int k0) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  auto issue = [&](int stage, int k0) {
+    u32x4* buf = lds[stage];
 #pragma unroll
-    for (int i = 0; i < kALoads; ++i) ra[i] = ld16(ap[i] + k0);
+    for (int i = 0; i < kALoads; ++i)
+      __builtin_amdgcn_global_load_lds(ap[i] + k0,
+                                       (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
+                                       16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < kBLoads; ++i) rb[i] = bp[i] ? ld16(bp[i] + k0) : u32x4{0, 0, 0, 0};
-  };
-  auto lstore = [&](u32x4* buf) {
-#pragma unroll
-    for (int i = 0; i < kALoads; ++i) buf[swz((tid >> 3) + 32 * i, jc)] = ra[i];
-#pragma unroll
-    for (int i = 0; i < kBLoads; ++i) buf[swz(kWM + (tid >> 3) + 32 * i, jc)] = rb[i];
+    for (int i = 0; i < kBLoads; ++i)
+      __builtin_amdgcn_global_load_lds(bp[i] + k0,
+                                       (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
+                                       16, 0, 0);
   };
 
   const int nk = K / kBK;
-  gload(0);
-  lstore(lds[0]);
-  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st)
+    if (st < nk) issue(st, st * kBK);
   const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
+  auto read_frags = [&](const u32x4* cur, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
+    const int j = 2 * ks + mk;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) fa[i] = cur[swz(wm * (kWM / 2) + 32 * i + mr, j)];
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) fb[t] = cur[swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
+  };
   for (int kt = 0; kt < nk; ++kt) {
-    const u32x4* cur = lds[kt & 1];
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
+    wait_ring<kStages - 2>(nk - 1 - kt);
+    ring_barrier();
+    if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, (kt + kStages - 1) * kBK);
+    const u32x4* cur = lds[kt % kStages];
+    u32x4 fa[2][kMT], fb[2][kNT];
+    read_frags(cur, 0, fa[0], fb[0]);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int j = 2 * ks + mk;
-      u32x4 fa[kMT], fb[kNT];
-#pragma unroll
-      for (int i = 0; i < kMT; ++i) fa[i] = cur[swz(wm * (kWM / 2) + 32 * i + mr, j)];
-#pragma unroll
-      for (int t = 0; t < kNT; ++t) fb[t] = cur[swz(kWM + wn * (kWT / 2) + 32 * t + mr, j)];
+    for (int ks = 0; ks < kKSteps; ++ks) {
+      if (ks + 1 < kKSteps) read_frags(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
 #pragma unroll
         for (int t = 0; t < kNT; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa[i]), as_bf16x8(fb[t]),
+          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa[ks & 1][i]),
+                                                              as_bf16x8(fb[ks & 1][t]),
                                                               acc[i][t], 0, 0, 0);
     }
-    if (kt + 1 < nk) lstore(lds[(kt + 1) & 1]);
-    __syncthreads();
+    // Schedule: the first k-step's fragment reads, then each later k-step's reads
+    // interleaved one-for-one with the previous k-step's MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, kMT + kNT, 0);
+#pragma unroll
+    for (int ks = 0; ks + 1 < kKSteps; ++ks) {
+#pragma unroll
+      for (int r = 0; r < kMT + kNT; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT - (kMT + kNT), 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT, 0);
   }
 
   // Epilogue.
   const int col = lane & 31, rq = 4 * (lane >> 5);
 #pragma unroll
   for (int t = 0; t < kNT; ++t) {
-    const int p = r0 + wn * (kWT / 2) + 32 * t + col;
+    const int p = r0 + wn * (kNT * 32) + 32 * t + col;
     if (p >= n) continue;
     uint16_t* orow = dst + static_cast<int64_t>(row0 + p) * dst_ld;
     if (GATEUP) {
@@ -247,7 +333,7 @@ int tiled_max_tiles(int64_t rows, int groups) {
 
 bool tiled_supported(const GroupWeights& gw) {
   return gw.H % kWM == 0 && gw.H % kBK == 0 && gw.I % (kWM / 2) == 0 &&
-         (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBK == 0;
+         (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBK == 0 && gw.I < (1 << 20);
 }
 
 hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
@@ -265,7 +351,7 @@ hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int
                                 void* act, hipStream_t s) {
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   const int n_wtiles = Imax / (kWM / 2);
-  tiled_kernel<true><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
+  tiled_kernel<true><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), gw.H, offsets, counts, perm_tok, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
@@ -275,7 +361,7 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
                              const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
                              int max_tiles, int64_t T, void* out, hipStream_t s) {
   const int n_wtiles = gw.H / kWM;
-  tiled_kernel<false><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
+  tiled_kernel<false><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(act), act_ld, offsets, counts, nullptr, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
   return hipGetLastError();
