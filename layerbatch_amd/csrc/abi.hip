@@ -89,6 +89,11 @@ static int32_t check_shape(const lbmoe_layer* layer) {
     return LBMOE_ERR_SHAPE;
   if (L.weight_dtype != LBMOE_W_BF16 && L.weight_dtype != LBMOE_W_FP8_E4M3)
     return LBMOE_ERR_DTYPE;
+  // fp8 kernels stream 256-byte (= 256 k) row segments holding two 128-k scale blocks
+  if (L.weight_dtype == LBMOE_W_FP8_E4M3 &&
+      (L.hidden_size % 256 != 0 || L.moe_intermediate_size % 256 != 0 ||
+       L.shared_intermediate_size % 256 != 0))
+    return LBMOE_ERR_SHAPE;
   return LBMOE_OK;
 }
 
@@ -183,7 +188,23 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   const GroupWeights gw = group_weights(L, with_shared, T);
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
-  if (is_fp8(L)) return LBMOE_ERR_DTYPE;
+  if (is_fp8(L)) {
+    // fp8: activations quantised per (row, 128 channels) before each GEMM
+    void* xq = at<void>(ws, w, R_XQ);
+    float* xs = at<float>(ws, w, R_XS);
+    void* actq = at<void>(ws, w, R_ACTQ);
+    float* acts = at<float>(ws, w, R_ACTS);
+    const int64_t rows = T * k + (with_shared ? T : 0);
+    LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
+    LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, counts, offsets, perm_tok, T, k, Imax, act, s));
+    LBMOE_TRY(ev->mark(s));
+    LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
+    LBMOE_TRY(launch_down_fp8(gw, actq, acts, Imax, counts, offsets, T, k, out, s));
+    LBMOE_TRY(ev->mark(s));
+    LBMOE_TRY(launch_combine(out, inv, topw, sgate, T, k, H, with_shared, y, s));
+    LBMOE_TRY(ev->mark(s));
+    return LBMOE_OK;
+  }
   if (use_tiled(gw, T, k)) {
     // prefill-sized batch: LDS-tiled MFMA GEMMs over a device-built token-tile list
     int32_t* tiles = at<int32_t>(ws, w, R_TILES);
@@ -401,7 +422,7 @@ static int32_t dense_mlp_layer(int32_t H, int32_t Is, int32_t dtype, lbmoe_layer
   L->hidden_size = H;
   L->num_experts = 1;
   L->top_k = 1;
-  L->moe_intermediate_size = 128;
+  L->moe_intermediate_size = 256;
   L->shared_intermediate_size = Is;
   L->weight_dtype = dtype;
   if (Is <= 0) return LBMOE_ERR_SHAPE;
@@ -441,15 +462,26 @@ int32_t lbmoe_dense_mlp(const void* gate_proj, const void* up_proj, const void* 
   const WsLayout w = ws_layout(L, T);
   if (workspace_bytes < w.total) return LBMOE_ERR_WORKSPACE;
   if ((st = check_device()) != LBMOE_OK) return st;
-  if (is_fp8(L)) return LBMOE_ERR_DTYPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   GroupWeights gw = group_weights(L, true, T);
   gw.g0 = L.num_experts;
   gw.groups = 1;
   gw.sh_row0 = 0;
   void* act = at<void>(workspace, w, R_ACT);
-  LBMOE_TRY(launch_gate_up_bf16(gw, x, nullptr, nullptr, nullptr, T, 1, Is, act, s));
-  LBMOE_TRY(launch_down_bf16(gw, act, Is, nullptr, nullptr, T, 1, out, s));
+  const int Imax = std::max(L.moe_intermediate_size, Is);
+  if (is_fp8(L)) {
+    void* xq = at<void>(workspace, w, R_XQ);
+    float* xs = at<float>(workspace, w, R_XS);
+    void* actq = at<void>(workspace, w, R_ACTQ);
+    float* acts = at<float>(workspace, w, R_ACTS);
+    LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
+    LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, nullptr, nullptr, nullptr, T, 1, Imax, act, s));
+    LBMOE_TRY(launch_quant_groups_fp8(act, T, Imax, Imax, actq, acts, s));
+    LBMOE_TRY(launch_down_fp8(gw, actq, acts, Imax, nullptr, nullptr, T, 1, out, s));
+    return LBMOE_OK;
+  }
+  LBMOE_TRY(launch_gate_up_bf16(gw, x, nullptr, nullptr, nullptr, T, 1, Imax, act, s));
+  LBMOE_TRY(launch_down_bf16(gw, act, Imax, nullptr, nullptr, T, 1, out, s));
   return LBMOE_OK;
 }
 

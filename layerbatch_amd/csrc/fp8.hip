@@ -91,3 +91,286 @@ hipError_t launch_quant_groups_fp8(const void* a, int64_t rows, int cols, int ld
 }
 
 }  // namespace lbmoe
+
+// ---- fp8 weight-streaming GEMMs -----------------------------------------------------------
+// Same scheme as the bf16 streaming kernels (stream_gemm.hip): a wave owns 16 weight rows per
+// tile (RA tiles) and streams them once per pass over its group's tokens, loading 4 rows x 256
+// contiguous bytes per instruction and transposing through a per-wave LDS scratch. With one
+// byte per element a 256-byte row segment is 256 k; it holds two 128-k scale blocks, each
+// one v_mfma_scale_f32_16x16x128_f8f6f4 (OCP e4m3 operands, unit E8M0 block scales): lane
+// (r, q) supplies 32 bytes k = 128c + 32q .. +32 of row r. The block product is scaled by
+// w_scale(row block, k block) * a_scale(token, k block) and added to the fp32 accumulator.
+namespace lbmoe {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+constexpr int kF8Block = 256;   // k (= bytes) per streamed block
+
+template <int RA, int TT>
+__device__ __forceinline__ void f8_load(const uint8_t* const (&ap)[RA][4],
+                                        const uint8_t* const (&bp)[TT][4], int k0,
+                                        u32x4 (&a)[RA][4], u32x4 (&b)[TT][4]) {
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[i][u] = ap[i][u] ? ld16_stream(ap[i][u] + k0) : u32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < TT; ++j)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[j][u] = bp[j][u] ? ld16(bp[j][u] + k0) : u32x4{0, 0, 0, 0};
+}
+
+__device__ __forceinline__ i32x8_t cat8(u32x4 lo, u32x4 hi) {
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// ws[i][c]: weight scale of tile i for scale block c of this k-block (wave-uniform);
+// xsc[j][c]: scale of this lane's token column in tile j.
+template <int RA, int TT>
+__device__ __forceinline__ void f8_mma(u32x4* __restrict__ lds, const u32x4 (&a)[RA][4],
+                                       const u32x4 (&b)[TT][4], const float (&ws)[RA][2],
+                                       const float (&xsc)[TT][2], f32x4 (&acc)[RA][TT]) {
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lds[(16 * i + 4 * u + q) * 16 + (r ^ (4 * u + q))] = a[i][u];
+#pragma unroll
+  for (int j = 0; j < TT; ++j)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lds[(16 * (RA + j) + 4 * u + q) * 16 + (r ^ (4 * u + q))] = b[j][u];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int j0 = 8 * c + 2 * q;
+    i32x8_t fa[RA], fb[TT];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+      fa[i] = cat8(lds[(16 * i + r) * 16 + (j0 ^ r)], lds[(16 * i + r) * 16 + ((j0 + 1) ^ r)]);
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+      fb[j] = cat8(lds[(16 * (RA + j) + r) * 16 + (j0 ^ r)],
+                   lds[(16 * (RA + j) + r) * 16 + ((j0 + 1) ^ r)]);
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j) {
+        const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            fa[i], fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        acc[i][j] += p * (ws[i][c] * xsc[j][c]);
+      }
+  }
+}
+
+template <int RA, int TT>
+__device__ __forceinline__ void f8_dot(u32x4* __restrict__ lds, const uint8_t* const (&ap)[RA][4],
+                                       const uint8_t* const (&bp)[TT][4],
+                                       const float* const (&wsp)[RA], const float* const (&xsp)[TT],
+                                       int K, f32x4 (&acc)[RA][TT]) {
+  // wsp[i]: the tile's row of block scales (K/128 entries); xsp[j]: the lane's token scales.
+  u32x4 a[RA][4], b[TT][4], an[RA][4], bn[TT][4];
+  f8_load<RA, TT>(ap, bp, 0, a, b);
+  for (int kb = 0; kb < K; kb += kF8Block) {
+    if (kb + kF8Block < K) f8_load<RA, TT>(ap, bp, kb + kF8Block, an, bn);
+    const int sb = kb / 128;
+    float ws[RA][2], xsc[TT][2];
+#pragma unroll
+    for (int i = 0; i < RA; ++i) {
+      ws[i][0] = wsp[i][sb];
+      ws[i][1] = wsp[i][sb + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      xsc[j][0] = xsp[j] ? xsp[j][sb] : 0.f;
+      xsc[j][1] = xsp[j] ? xsp[j][sb + 1] : 0.f;
+    }
+    f8_mma<RA, TT>(lds, a, b, ws, xsc, acc);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int i = 0; i < RA; ++i) a[i][u] = an[i][u];
+#pragma unroll
+      for (int j = 0; j < TT; ++j) b[j][u] = bn[j][u];
+    }
+  }
+}
+
+template <int RA, int TT>
+__device__ __forceinline__ void zero_acc8(f32x4 (&acc)[RA][TT]) {
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < TT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// gate_up: wave (channel block cb, group g) -> act[row, 16cb .. 16cb+15] (bf16).
+template <int TT>
+__global__ __launch_bounds__(64) void gate_up_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ xq,
+                                                         const float* __restrict__ xs,
+                                                         const int32_t* __restrict__ counts,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ perm_tok,
+                                                         int T, int act_ld, uint16_t* __restrict__ act) {
+  __shared__ u32x4 lds[(2 + TT) * 256];
+  const int g = gw.g0 + blockIdx.y;
+  const bool shared = g == gw.E;
+  const int Ig = shared ? gw.Is : gw.I;
+  const int c0 = blockIdx.x * 16;
+  if (c0 >= Ig) return;
+  const int n = shared ? T : counts[g];
+  if (n == 0) return;
+  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  const int H = gw.H, nkb = H / 128;
+  const int lane = lane_id(), r = lane & 15, q = lane >> 4;
+  const uint8_t* wgt;
+  const uint8_t* wup;
+  const float* sg;
+  const float* su;
+  if (shared) {
+    wgt = static_cast<const uint8_t*>(gw.sh_gate);
+    wup = static_cast<const uint8_t*>(gw.sh_up);
+    sg = gw.sh_gate_scale + static_cast<int64_t>(c0 / 128) * nkb;
+    su = gw.sh_up_scale + static_cast<int64_t>(c0 / 128) * nkb;
+  } else {
+    wgt = static_cast<const uint8_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
+    wup = wgt + static_cast<int64_t>(gw.I) * H;
+    const float* s0 = gw.gate_up_scale + static_cast<int64_t>(g) * (2 * gw.I / 128) * nkb;
+    sg = s0 + static_cast<int64_t>(c0 / 128) * nkb;
+    su = s0 + static_cast<int64_t>((gw.I + c0) / 128) * nkb;
+  }
+  const uint8_t* ap[2][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ap[0][u] = wgt + static_cast<int64_t>(c0 + 4 * u + q) * H + 16 * r;
+    ap[1][u] = wup + static_cast<int64_t>(c0 + 4 * u + q) * H + 16 * r;
+  }
+  const float* wsp[2] = {sg, su};
+  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+    const uint8_t* bp[TT][4];
+    const float* xsp[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + 16 * j + 4 * u + q;
+        const int tok = p < n ? (shared ? p : perm_tok[row0 + p]) : -1;
+        bp[j][u] = tok >= 0 ? xq + static_cast<int64_t>(tok) * H + 16 * r : nullptr;
+      }
+      const int pc = p0 + 16 * j + r;     // this lane's accumulator column
+      const int tc = pc < n ? (shared ? pc : perm_tok[row0 + pc]) : -1;
+      xsp[j] = tc >= 0 ? xs + static_cast<int64_t>(tc) * nkb : nullptr;
+    }
+    f32x4 acc[2][TT];
+    zero_acc8(acc);
+    f8_dot<2, TT>(lds, ap, bp, wsp, xsp, H, acc);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      const int p = p0 + 16 * j + r;
+      if (p >= n) continue;
+      float a[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) a[v] = silu(acc[0][j][v]) * acc[1][j][v];
+      *reinterpret_cast<u32x2*>(act + static_cast<int64_t>(row0 + p) * act_ld + c0 + 4 * q) =
+          u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+    }
+  }
+}
+
+// down: wave (row block hb of 32, group g) -> out[row, 32hb .. 32hb+31] (bf16).
+template <int TT>
+__global__ __launch_bounds__(64) void down_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ aq,
+                                                      const float* __restrict__ as, int act_ld,
+                                                      const int32_t* __restrict__ counts,
+                                                      const int32_t* __restrict__ offsets, int T,
+                                                      uint16_t* __restrict__ out) {
+  __shared__ u32x4 lds[(2 + TT) * 256];
+  const int g = gw.g0 + blockIdx.y;
+  const bool shared = g == gw.E;
+  const int Ig = shared ? gw.Is : gw.I;
+  const int n = shared ? T : counts[g];
+  if (n == 0) return;
+  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  const int H = gw.H, h0 = blockIdx.x * 32;
+  const int nkb = Ig / 128, nsa = act_ld / 128;
+  const int lane = lane_id(), r = lane & 15, q = lane >> 4;
+  const uint8_t* wd;
+  const float* sd;
+  if (shared) {
+    wd = static_cast<const uint8_t*>(gw.sh_down);
+    sd = gw.sh_down_scale + static_cast<int64_t>(h0 / 128) * nkb;
+  } else {
+    wd = static_cast<const uint8_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
+    sd = gw.down_scale + (static_cast<int64_t>(g) * (H / 128) + h0 / 128) * nkb;
+  }
+  const uint8_t* ap[2][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ap[0][u] = wd + static_cast<int64_t>(h0 + 4 * u + q) * Ig + 16 * r;
+    ap[1][u] = wd + static_cast<int64_t>(h0 + 16 + 4 * u + q) * Ig + 16 * r;
+  }
+  const float* wsp[2] = {sd, sd};
+  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+    const uint8_t* bp[TT][4];
+    const float* xsp[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + 16 * j + 4 * u + q;
+        bp[j][u] = p < n ? aq + static_cast<int64_t>(row0 + p) * act_ld + 16 * r : nullptr;
+      }
+      const int pc = p0 + 16 * j + r;
+      xsp[j] = pc < n ? as + static_cast<int64_t>(row0 + pc) * nsa : nullptr;
+    }
+    f32x4 acc[2][TT];
+    zero_acc8(acc);
+    f8_dot<2, TT>(lds, ap, bp, wsp, xsp, Ig, acc);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      const int p = p0 + 16 * j + r;
+      if (p >= n) continue;
+      uint16_t* orow = out + static_cast<int64_t>(row0 + p) * H + h0 + 4 * q;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        *reinterpret_cast<u32x2*>(orow + 16 * i) =
+            u32x2{pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3])};
+    }
+  }
+}
+
+static int pick_tt8(const GroupWeights& gw, int64_t T, int k) {
+  const double avg = gw.g0 < gw.E ? static_cast<double>(T) * k / gw.E : static_cast<double>(T);
+  return avg <= 12.0 ? 1 : (avg <= 28.0 ? 2 : 4);
+}
+
+hipError_t launch_gate_up_fp8(const GroupWeights& gw, const void* xq, const float* xs,
+                              const int32_t* counts, const int32_t* offsets,
+                              const int32_t* perm_tok, int64_t T, int k, int act_ld, void* act,
+                              hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const dim3 grid(Imax / 16, gw.groups);
+  const auto* x8 = static_cast<const uint8_t*>(xq);
+  auto* a = static_cast<uint16_t*>(act);
+  const int Ti = static_cast<int>(T);
+  switch (pick_tt8(gw, T, k)) {
+    case 1: gate_up_fp8_kernel<1><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
+    case 2: gate_up_fp8_kernel<2><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
+    default: gate_up_fp8_kernel<4><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_down_fp8(const GroupWeights& gw, const void* actq, const float* acts,
+                           int act_ld, const int32_t* counts, const int32_t* offsets,
+                           int64_t T, int k, void* out, hipStream_t s) {
+  const dim3 grid(gw.H / 32, gw.groups);
+  const auto* a8 = static_cast<const uint8_t*>(actq);
+  auto* o = static_cast<uint16_t*>(out);
+  const int Ti = static_cast<int>(T);
+  switch (pick_tt8(gw, T, k)) {
+    case 1: down_fp8_kernel<1><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
+    case 2: down_fp8_kernel<2><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
+    default: down_fp8_kernel<4><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lbmoe

@@ -92,10 +92,10 @@ hipError_t launch_quant_groups_fp8(const void* a, int64_t rows, int cols, int ld
                                    float* scale, hipStream_t s);
 hipError_t launch_gate_up_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                               const int32_t* counts, const int32_t* offsets,
-                              const int32_t* perm_tok, int64_t T, int act_ld, void* act,
+                              const int32_t* perm_tok, int64_t T, int k, int act_ld, void* act,
                               hipStream_t s);
 hipError_t launch_down_fp8(const GroupWeights& gw, const void* actq, const float* acts,
                            int act_ld, const int32_t* counts, const int32_t* offsets,
-                           int64_t T, void* out, hipStream_t s);
+                           int64_t T, int k, void* out, hipStream_t s);
 
 }  // namespace lbmoe

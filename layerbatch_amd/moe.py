@@ -73,7 +73,7 @@ class Qwen3_5TopKRouter(nn.Module):
         E, H = self.weight.shape
         L = LbmoeLayer()
         L.hidden_size, L.num_experts, L.top_k = H, E, self.top_k
-        L.moe_intermediate_size = 128           # routed-expert sizes are unused by the router
+        L.moe_intermediate_size = 256           # routed-expert sizes are unused by the router
         L.gate_weight = self.weight.data_ptr()
         if self.logit_bias is not None:
             _require(self.logit_bias, "logit_bias", torch.float32, 1)

@@ -1,0 +1,108 @@
+"""GPU parity of the fp8 (OCP e4m3fn) variant against the CPU oracle's dequantised fp32 path."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from layerbatch_amd import _lib
+from layerbatch_amd.synth import MoEShape, make_layer, make_x
+from oracle import moe as om
+from tests import gpu_checks as gc
+from tests.helpers import bf16_bits_of, layer_np, to_np
+from tests.test_gpu_parity import _block, _region
+
+pytestmark = pytest.mark.gpu
+
+
+def test_quantize_blocks_bit_exact(gpu):
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn((3, 256, 384), generator=g) * 0.02)
+    w[1, :128, :128] = 0.0                              # an all-zero block: scale 1, codes 0
+    w[2, 5, 7] = 3.0e4                                  # a large outlier
+    wb = w.to(torch.bfloat16)
+    from layerbatch_amd.moe import _quantize_blocks
+    q, s = _quantize_blocks(wb.to(gpu))
+    torch.cuda.synchronize()
+    q_ref, s_ref = om.quant_blocks(to_np(wb))
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+def _fp8_oracle(wn, q, xn, idx, topw, shared):
+    y = om.experts_fp8(xn, idx, topw, q["wgu_q"], q["wgu_s"], q["wd_q"], q["wd_s"])
+    if shared:
+        gsh = om.shared_gate(xn, wn["sh_gate_w"]).astype(np.float64)
+        y = y + gsh[:, None] * om.shared_expert_fp8(xn, q["sh_gate_q"], q["sh_gate_s"], q["sh_up_q"],
+                                                    q["sh_up_s"], q["sh_down_q"], q["sh_down_s"])
+    return y
+
+
+def _run_fp8(shape, T, device, seed=0, sample=None):
+    w, g = make_layer(shape, seed=seed)
+    x = make_x(g, T, shape.hidden_size)
+    blk = _block(shape, {k_: v.to(device) for k_, v in w.items()}, device)
+    blk.quantize_fp8_()
+    xd = x.to(device)
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=device)
+    y = blk(xd, workspace=ws)
+    torch.cuda.synchronize()
+    k = shape.top_k
+    idx = to_np(_region(blk, ws, T, "topk_idx", torch.int32, (T, k))).astype(np.int64)
+    topw = to_np(_region(blk, ws, T, "topk_w", torch.bfloat16, (T, k)))
+    logits = _region(blk, ws, T, "logits", torch.bfloat16, (T, shape.num_experts))
+    gc.check_route(idx, bf16_bits_of(_region(blk, ws, T, "topk_w", torch.bfloat16, (T, k))),
+                   to_np(logits), None, k)
+    ex = blk.experts
+    q = {"wgu_q": ex.gate_up_q.cpu().numpy(), "wgu_s": ex.gate_up_scale.cpu().numpy(),
+         "wd_q": ex.down_q.cpu().numpy(), "wd_s": ex.down_scale.cpu().numpy()}
+    wn = layer_np(w)
+    # the GPU's quantised weights must be the oracle's quantisation of the bf16 weights
+    q_ref, s_ref = om.quant_blocks(wn["gate_up"])
+    np.testing.assert_array_equal(q["wgu_q"], q_ref)
+    np.testing.assert_array_equal(q["wgu_s"], s_ref)
+    shared = shape.shared_expert_intermediate_size > 0
+    if shared:
+        for n in ("gate", "up", "down"):
+            cq, cs = blk.shared_expert.q[n]
+            q[f"sh_{n}_q"], q[f"sh_{n}_s"] = cq.cpu().numpy(), cs.cpu().numpy()
+    xn = to_np(x)
+    rows = np.arange(T) if sample is None else np.unique(
+        np.random.default_rng(seed).choice(T, size=min(sample, T), replace=False))
+    y_ref = _fp8_oracle(wn, q, xn[rows], idx[rows], topw[rows], shared)
+    err = gc.check_output(to_np(y)[rows], y_ref, gc.TOL_FP8)
+    # and the fp8 layer stays close to the bf16 layer it approximates
+    y_bf = gc.block_reference(xn[rows], wn, idx[rows], topw[rows], k, shared=True if shared else None)
+    assert om.rel_err(to_np(y)[rows], y_bf) < 0.1
+    return err
+
+
+@pytest.mark.parametrize("T", [1, 64, 200])
+def test_fp8_block_small(gpu, T):
+    _run_fp8(MoEShape(1024, 16, 2, 512, 0), T, gpu, seed=T)
+
+
+def test_fp8_block_shared(gpu):
+    _run_fp8(MoEShape(1024, 32, 4, 256, 512), 96, gpu, seed=5)
+
+
+def test_fp8_dense_mlp(gpu):
+    shape = MoEShape(1024, 8, 2, 256, 512)
+    w, g = make_layer(shape, seed=6)
+    x = make_x(g, 70, 1024)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    blk.quantize_fp8_()
+    out = blk.shared_expert(x.to(gpu))
+    se = blk.shared_expert
+    qq = {n: (se.q[n][0].cpu().numpy(), se.q[n][1].cpu().numpy()) for n in ("gate", "up", "down")}
+    ref = om.shared_expert_fp8(to_np(x), *qq["gate"], *qq["up"], *qq["down"])
+    gc.check_output(to_np(out), ref, gc.TOL_FP8)
+
+
+def test_fp8_rejects_unsupported_width(gpu, lbmoe):
+    from layerbatch_amd._lib import LbmoeLayer
+    L = LbmoeLayer()
+    L.hidden_size, L.num_experts, L.top_k = 1024, 8, 2
+    L.moe_intermediate_size, L.weight_dtype = 384, _lib.LBMOE_W_FP8_E4M3
+    n = ctypes.c_size_t(0)
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), 4, ctypes.byref(n)) == -2
