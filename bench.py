@@ -78,7 +78,7 @@ class HipEvents:
         return ms.value
 
 
-def layer_inputs(shape, T, seed, zipf, device):
+def layer_inputs(shape, T, seed, zipf, device, fp8=False):
     import torch
     from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
     from layerbatch_amd.synth import make_layer, make_x, zipf_bias
@@ -98,6 +98,8 @@ def layer_inputs(shape, T, seed, zipf, device):
             blk.shared_expert_gate.weight.copy_(w["sh_gate_w"])
     if zipf:
         blk.gate.logit_bias = zipf_bias(g, shape.num_experts, device=device)
+    if fp8:
+        blk.quantize_fp8_()
     del w
     return blk, x
 

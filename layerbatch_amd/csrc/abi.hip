@@ -196,10 +196,22 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     float* acts = at<float>(ws, w, R_ACTS);
     const int64_t rows = T * k + (with_shared ? T : 0);
     LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
-    LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, counts, offsets, perm_tok, T, k, Imax, act, s));
-    LBMOE_TRY(ev->mark(s));
-    LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
-    LBMOE_TRY(launch_down_fp8(gw, actq, acts, Imax, counts, offsets, T, k, out, s));
+    if (use_tiled(gw, T, k)) {
+      int32_t* tiles = at<int32_t>(ws, w, R_TILES);
+      const int max_tiles = tiled_max_tiles(rows, gw.groups);
+      LBMOE_TRY(launch_build_tiles(counts, E, with_shared, T, max_tiles, tiles, s));
+      LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, counts, offsets, perm_tok, tiles, max_tiles,
+                                         T, Imax, act, s));
+      LBMOE_TRY(ev->mark(s));
+      LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
+      LBMOE_TRY(launch_down_tiled_fp8(gw, actq, acts, Imax, counts, offsets, tiles, max_tiles, T,
+                                      out, s));
+    } else {
+      LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, counts, offsets, perm_tok, T, k, Imax, act, s));
+      LBMOE_TRY(ev->mark(s));
+      LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
+      LBMOE_TRY(launch_down_fp8(gw, actq, acts, Imax, counts, offsets, T, k, out, s));
+    }
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_combine(out, inv, topw, sgate, T, k, H, with_shared, y, s));
     LBMOE_TRY(ev->mark(s));
@@ -380,7 +392,7 @@ int32_t lbmoe_permute(const void* topk_idx, int32_t idx_bytes, int64_t T, int32_
   size_t h, b, l, total;
   perm_scratch_layout(T, k, E, &h, &b, &l, &total);
   if (T > 0 && (!topk_idx || !perm_tok || !perm_slot || !inv)) return LBMOE_ERR_NULL;
-  if (T * k > kPermChunk && (!workspace || workspace_bytes < total)) return LBMOE_ERR_WORKSPACE;
+  if (T * k > kPermSingle && (!workspace || workspace_bytes < total)) return LBMOE_ERR_WORKSPACE;
   int32_t st = check_device();
   if (st != LBMOE_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);

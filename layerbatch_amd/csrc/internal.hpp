@@ -9,8 +9,10 @@
 
 namespace lbmoe {
 
-// Entries of the permutation handled by one block of the count/scatter kernels.
-constexpr int kPermChunk = 1024;
+// Permutations of at most kPermSingle entries run in one wave; larger ones in chunks of
+// kPermChunk entries, one wave per chunk.
+constexpr int kPermSingle = 1024;
+constexpr int kPermChunk = 256;
 
 inline int64_t perm_blocks(int64_t V) { return (V + kPermChunk - 1) / kPermChunk; }
 
@@ -85,6 +87,17 @@ hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
                              const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
                              int max_tiles, int64_t T, void* out, hipStream_t s);
+hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
+                                    const int32_t* counts, const int32_t* offsets,
+                                    const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
+                                    int64_t T, int act_ld, void* act, hipStream_t s);
+hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const float* acts,
+                                 int act_ld, const int32_t* counts, const int32_t* offsets,
+                                 const int32_t* tiles, int max_tiles, int64_t T, void* out,
+                                 hipStream_t s);
+bool tiled_router_supported(int E, int H);
+hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
+                                      void* logits, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);
 hipError_t launch_quant_blocks_fp8(const void* w, int64_t batch, int N, int K, void* q,
                                    float* scale, hipStream_t s);

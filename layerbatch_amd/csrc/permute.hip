@@ -5,14 +5,15 @@
 // row-major. Entries are visited in slot-major order v = s*T + t, so a stable counting sort
 // on the expert id yields exactly the key (expert, slot, token).
 //
-// Three passes, integer-only and deterministic:
-//   count   one wave per chunk of kPermChunk entries: stable rank of every entry among the
-//           chunk's entries of the same expert (64-lane ballot matching on the expert bits),
-//           per-chunk histogram hist[e][chunk].
-//   scan    one workgroup: exclusive scan of hist in (expert, chunk) order -> base[e][chunk],
-//           counts[e], offsets[e].
-//   scatter one wave per chunk: pos = base[e][chunk] + rank -> perm_tok, perm_slot, inv.
-// When all entries fit one chunk the three passes run in a single one-wave kernel.
+// Integer-only and deterministic:
+//   count     one wave per chunk of kPermChunk entries: stable rank of every entry among the
+//             chunk's entries of the same expert (64-lane ballot matching on the expert
+//             bits), per-chunk histogram hist[e][chunk].
+//   per-expert one wave per expert: exclusive scan of hist[e][*] -> base[e][chunk], total[e].
+//   offsets   one workgroup: exclusive scan of the totals -> counts[e], offsets[e].
+//   scatter   one wave per chunk: pos = offsets[e] + base[e][chunk] + rank -> perm_tok,
+//             perm_slot, inv.
+// Up to kPermSingle entries (decode-sized batches) run all of it in a single one-wave kernel.
 // Entries whose expert id lies outside [0, E) are left out of every list and get inv = -1.
 #include "common.hpp"
 #include "internal.hpp"
@@ -70,6 +71,7 @@ __device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E,
 }
 
 constexpr int kRounds = kPermChunk / kWave;
+constexpr int kSingleRounds = kPermSingle / kWave;
 
 template <int IB>
 __global__ __launch_bounds__(64) void perm_count(const void* idx, int T, int k, int E,
@@ -91,20 +93,40 @@ __global__ __launch_bounds__(64) void perm_count(const void* idx, int T, int k, 
   for (int e = lane; e < E; e += kWave) hist[static_cast<int64_t>(e) * nblk + b] = run[e];
 }
 
-// Exclusive scan of n ints in place order (one workgroup of 1024 threads).
-__global__ __launch_bounds__(1024) void perm_scan(const int32_t* hist, int E, int nblk, int V,
-                                                  int32_t* base, int32_t* counts,
-                                                  int32_t* offsets) {
-  __shared__ int wsum[16];
-  const int n = E * nblk;
-  const int tid = threadIdx.x;
-  const int per = (n + 1023) / 1024;
-  const int lo = min(n, tid * per), hi = min(n, lo + per);
+// Per expert (one wave each): exclusive scan of its per-chunk counts, and its total.
+__global__ __launch_bounds__(64) void perm_expert_scan(const int32_t* __restrict__ hist, int nblk,
+                                                       int32_t* __restrict__ base,
+                                                       int32_t* __restrict__ totals) {
+  const int e = blockIdx.x, lane = lane_id();
+  const int per = (nblk + kWave - 1) / kWave;
+  const int lo = min(nblk, lane * per), hi = min(nblk, lo + per);
+  const int32_t* h = hist + static_cast<int64_t>(e) * nblk;
   int local = 0;
-  for (int i = lo; i < hi; ++i) local += hist[i];
-  // inclusive scan of `local` across the block
+  for (int b = lo; b < hi; ++b) local += h[b];
   int incl = local;
-  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  int run = incl - local;
+  int32_t* bs = base + static_cast<int64_t>(e) * nblk;
+  for (int b = lo; b < hi; ++b) {
+    const int c = h[b];
+    bs[b] = run;
+    run += c;
+  }
+  if (lane == 63) totals[e] = incl;
+}
+
+// Exclusive scan of the E expert totals (one workgroup of 1024 threads, E <= 1024).
+__global__ __launch_bounds__(1024) void perm_offsets(const int32_t* __restrict__ totals, int E,
+                                                     int32_t* __restrict__ counts,
+                                                     int32_t* __restrict__ offsets) {
+  __shared__ int wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = tid < E ? totals[tid] : 0;
+  int incl = c;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const int y = __shfl_up(incl, o, kWave);
@@ -122,17 +144,10 @@ __global__ __launch_bounds__(1024) void perm_scan(const int32_t* hist, int E, in
     if (lane < 16) wsum[lane] = w;
   }
   __syncthreads();
-  int run = incl - local + (wave > 0 ? wsum[wave - 1] : 0);
-  for (int i = lo; i < hi; ++i) {
-    base[i] = run;
-    run += hist[i];
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += 1024) {
-    const int o0 = base[static_cast<int64_t>(e) * nblk];
-    const int o1 = (e + 1 < E) ? base[static_cast<int64_t>(e + 1) * nblk] : wsum[15];
-    offsets[e] = o0;
-    counts[e] = o1 - o0;
+  const int excl = incl - c + (wave > 0 ? wsum[wave - 1] : 0);
+  if (tid < E) {
+    counts[tid] = c;
+    offsets[tid] = excl;
   }
   if (tid == 0) offsets[E] = wsum[15];
 }
@@ -140,8 +155,9 @@ __global__ __launch_bounds__(1024) void perm_scan(const int32_t* hist, int E, in
 template <int IB>
 __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k, int E, int V,
                                                    int nblk, const int32_t* base,
-                                                   const int32_t* lrank, int32_t* perm_tok,
-                                                   int32_t* perm_slot, int32_t* inv) {
+                                                   const int32_t* offsets, const int32_t* lrank,
+                                                   int32_t* perm_tok, int32_t* perm_slot,
+                                                   int32_t* inv) {
   const int lane = lane_id();
   const int b = blockIdx.x;
   for (int r = 0; r < kRounds; ++r) {
@@ -155,14 +171,14 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
       inv[ts] = -1;
       continue;
     }
-    const int pos = base[static_cast<int64_t>(e) * nblk + b] + lrank[v];
+    const int pos = offsets[e] + base[static_cast<int64_t>(e) * nblk + b] + lrank[v];
     perm_tok[pos] = t;
     perm_slot[pos] = s;
     inv[ts] = pos;
   }
 }
 
-// Whole permutation in one wave when V <= kPermChunk (decode-sized batches).
+// Whole permutation in one wave when V <= kPermSingle (decode-sized batches).
 template <int IB>
 __global__ __launch_bounds__(64) void perm_single(const void* idx, int T, int k, int E,
                                                   int nbits, int V, int32_t* counts,
@@ -173,8 +189,8 @@ __global__ __launch_bounds__(64) void perm_single(const void* idx, int T, int k,
   const int lane = lane_id();
   for (int e = lane; e < E; e += kWave) run[e] = 0;
   __syncthreads();
-  int ee[kRounds], rk[kRounds];
-  rank_chunk<IB, kRounds>(idx, T, k, E, nbits, V, 0, run, ee, rk);
+  int ee[kSingleRounds], rk[kSingleRounds];
+  rank_chunk<IB, kSingleRounds>(idx, T, k, E, nbits, V, 0, run, ee, rk);
   __syncthreads();
   // exclusive scan of run[0..E) by one wave: each lane owns a contiguous slice
   const int per = (E + kWave - 1) / kWave;
@@ -197,7 +213,7 @@ __global__ __launch_bounds__(64) void perm_single(const void* idx, int T, int k,
   if (lane == 63) offsets[E] = incl;
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
+  for (int r = 0; r < kSingleRounds; ++r) {
     const int v = r * kWave + lane;
     if (v < V) {
       const int s = v / T;
@@ -239,17 +255,19 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
                                    hipStream_t s) {
   const int V = static_cast<int>(T * k);
   const int nbits = bits_for(E);
-  if (V <= kPermChunk) {
+  if (V <= kPermSingle) {
     perm_single<IB><<<1, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, counts, offsets,
                                      perm_tok, perm_slot, inv);
     return hipGetLastError();
   }
+  // hist, base: E x nblk; lrank: V; the totals reuse the counts array until perm_offsets
   const int nblk = static_cast<int>(perm_blocks(V));
   perm_count<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist,
                                      lrank);
-  perm_scan<<<1, 1024, 0, s>>>(hist, E, nblk, V, base, counts, offsets);
-  perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, lrank,
-                                       perm_tok, perm_slot, inv);
+  perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
+  perm_offsets<<<1, 1024, 0, s>>>(counts, E, counts, offsets);
+  perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, offsets,
+                                       lrank, perm_tok, perm_slot, inv);
   return hipGetLastError();
 }
 

@@ -245,8 +245,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
   }
 }
 
+// Token count from which the router logits run as an LDS-tiled MFMA GEMM.
+constexpr int64_t kTiledRouterMinTokens = 1024;
+
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
                                 void* logits, hipStream_t s) {
+  if (T >= kTiledRouterMinTokens && tiled_router_supported(E, H))
+    return launch_router_logits_tiled(x, wg, T, E, H, logits, s);
   const dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
   router_logits_kernel<<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x),
                                             static_cast<const uint16_t*>(wg),

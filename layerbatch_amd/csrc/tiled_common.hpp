@@ -1,0 +1,48 @@
+// Helpers shared by the LDS-tiled kernels (tiled_gemm.hip, tiled_fp8.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace lbmoe {
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Workgroup barrier for the LDS ring: the wave's LDS reads are complete (lgkmcnt 0) and its
+// own global->LDS copies were waited for by the caller; unlike __syncthreads this does not
+// drain the copies still in flight for later stages. The signal fences keep the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((0x3f & 0xf) | ((0x3f >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Wait until the oldest in-flight stage's copies (L copies per stage and wave) have landed
+// while the copies of up to min(S, later) younger stages stay in flight (vector-memory
+// operations complete in order).
+template <int S, int L>
+__device__ __forceinline__ void wait_ring(int later) {
+  static_assert(S * L < 64, "vmcnt holds at most 63 outstanding operations");
+  if constexpr (S <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (later >= S) wait_vmcnt<S * L>();
+    else wait_ring<S - 1, L>(later);
+  }
+}
+
+// Workgroup b of a grid of nblk (a multiple of 8) runs on XCD b % 8; consecutive logical
+// indices are given to the same XCD so that tiles sharing operands share its L2.
+__device__ __forceinline__ int xcd_logical_block(int b, int nblk) {
+  return (b % 8) * (nblk / 8) + b / 8;
+}
+
+inline unsigned round8(int64_t v) { return static_cast<unsigned>((v + 7) / 8 * 8); }
+
+}  // namespace lbmoe

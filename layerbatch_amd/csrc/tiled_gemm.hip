@@ -22,6 +22,7 @@
 // same kWM/4 channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
 #include "internal.hpp"
+#include "tiled_common.hpp"
 
 namespace lbmoe {
 
@@ -67,38 +68,6 @@ constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
 static_assert(kChunks == 4 || kChunks == 8, "kBK must be 32 or 64");
 __device__ __forceinline__ int swz(int r, int j) {
   return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
-}
-
-// Workgroup barrier for the LDS ring: the wave's LDS reads are complete (lgkmcnt 0) and its
-// own global->LDS copies were waited for by the caller; unlike __syncthreads this does not
-// drain the copies still in flight for later stages. The signal fences keep the compiler from
-// moving LDS accesses across it.
-__device__ __forceinline__ void ring_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt((0x3f & 0xf) | ((0x3f >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
-// Wait until the oldest in-flight stage's copies have landed while the copies of up to
-// min(S, later) younger stages stay in flight (vector-memory ops complete in order).
-template <int S>
-__device__ __forceinline__ void wait_ring(int later) {
-  constexpr int L = kALoads + kBLoads;
-  static_assert(S * L < 64, "vmcnt holds at most 63 outstanding operations");
-  if constexpr (S <= 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (later >= S) wait_vmcnt<S * L>();
-    else wait_ring<S - 1>(later);
-  }
 }
 
 // ---- tile list -------------------------------------------------------------------------------
@@ -151,7 +120,12 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
 }
 
 // ---- the tiled kernel ----------------------------------------------------------------------
-template <bool GATEUP>
+// MODE kDown: out[row, h] = act[row] . Wd_g[h];  kGateUp: act[row, c] = silu(gate) * up;
+// kRouter: logits[t, e] = x[t] . Wg[e] over token tiles t0 = 128 * tile (no tile list;
+// gw.gate_up holds the router weight, gw.E its row count).
+enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
+
+template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_TILE_WPE, LBMOE_TILE_WPE))) void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src,
                                                     int src_ld, const int32_t* __restrict__ offsets,
                                                     const int32_t* __restrict__ counts,
@@ -159,23 +133,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
                                                     const int32_t* __restrict__ tiles,
                                                     int max_tiles, int n_wtiles, int T,
                                                     uint16_t* __restrict__ dst, int dst_ld) {
+  constexpr bool GATEUP = MODE == kGateUp, ROUTER = MODE == kRouter;
   __shared__ u32x4 lds[kStages][kStageU4];
   // XCD-aware order: hardware hands out workgroup b to XCD b % 8.
-  const int nblk = gridDim.x;
-  const int b = blockIdx.x;
-  const int per_xcd = nblk / 8;                      // nblk is a multiple of 8
-  const int logical = (b % 8) * per_xcd + b / 8;
+  const int logical = xcd_logical_block(blockIdx.x, gridDim.x);
   const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  if (ti >= tiles[2 * max_tiles]) return;
-  const int g = tiles[2 * ti], r0 = tiles[2 * ti + 1];
-  const bool shared = g == gw.E;
+  int g = 0, r0, n, row0;
+  if (ROUTER) {
+    if (ti * kWT >= T) return;
+    r0 = ti * kWT;
+    n = T;
+    row0 = 0;
+  } else {
+    if (ti >= tiles[2 * max_tiles]) return;
+    g = tiles[2 * ti];
+    r0 = tiles[2 * ti + 1];
+  }
+  const bool shared = !ROUTER && g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int H = gw.H;
-  const int n = shared ? T : counts[g];
-  const int row0 = shared ? gw.sh_row0 : offsets[g];
-  const int K = GATEUP ? H : Ig;
-  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel (gate_up) / column (down)
-  if (c0 >= (GATEUP ? Ig : H)) return;
+  if (!ROUTER) {
+    n = shared ? T : counts[g];
+    row0 = shared ? gw.sh_row0 : offsets[g];
+  }
+  const int K = (GATEUP || ROUTER) ? H : Ig;
+  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel / output column
+  if (c0 >= (GATEUP ? Ig : (ROUTER ? gw.E : H))) return;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w % kWavesM, wn = w / kWavesM;
@@ -193,6 +176,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
       wbase = static_cast<const uint16_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
       wup = wbase + static_cast<int64_t>(gw.I) * H;
     }
+  } else if (ROUTER) {
+    wbase = static_cast<const uint16_t*>(gw.gate_up);
   } else {
     wbase = shared ? static_cast<const uint16_t*>(gw.sh_down)
                    : static_cast<const uint16_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
@@ -209,6 +194,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
       const int half = row / (kWM / 2), sub = row % (kWM / 2);
       base = sub < kWM / 4 ? wbase : wup;
       grow = c0 + half * (kWM / 4) + (sub % (kWM / 4));
+    } else if (ROUTER) {
+      grow = min(c0 + row, gw.E - 1);      // rows past E repeat a valid row; not stored
     } else {
       grow = c0 + row;
     }
@@ -221,7 +208,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
     const int row = kWM + lt;
     const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
     const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
-    const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
+    const int srow = ROUTER ? p : (GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p);
     bp[i] = src + static_cast<int64_t>(srow) * src_ld + 8 * j;
   }
 
@@ -261,7 +248,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
     for (int t = 0; t < kNT; ++t) fb[t] = cur[swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
   };
   for (int kt = 0; kt < nk; ++kt) {
-    wait_ring<kStages - 2>(nk - 1 - kt);
+    wait_ring<kStages - 2, kALoads + kBLoads>(nk - 1 - kt);
     ring_barrier();
     if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, (kt + kStages - 1) * kBK);
     const u32x4* cur = lds[kt % kStages];
@@ -312,6 +299,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
           const int ch = c0 + wm * (kWM / 4) + 32 * i + 8 * v4 + rq;
           *reinterpret_cast<u32x2*>(orow + ch) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
+    } else if (ROUTER) {
+      const int E = gw.E;
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int e = c0 + wm * (kWM / 2) + 32 * i + 8 * v4 + rq;
+          if (e + 3 < E && (E & 3) == 0) {
+            *reinterpret_cast<u32x2*>(orow + e) =
+                u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
+                      pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (e + v < E) orow[e + v] = static_cast<uint16_t>(f2bf(acc[i][t][4 * v4 + v]));
+          }
+        }
     } else {
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
@@ -343,7 +347,6 @@ hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t
   return hipGetLastError();
 }
 
-static unsigned round8(int64_t v) { return static_cast<unsigned>((v + 7) / 8 * 8); }
 
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
                                 const int32_t* offsets, const int32_t* perm_tok,
@@ -351,7 +354,7 @@ hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int
                                 void* act, hipStream_t s) {
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   const int n_wtiles = Imax / (kWM / 2);
-  tiled_kernel<true><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
+  tiled_kernel<kGateUp><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), gw.H, offsets, counts, perm_tok, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
@@ -361,9 +364,29 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
                              const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
                              int max_tiles, int64_t T, void* out, hipStream_t s) {
   const int n_wtiles = gw.H / kWM;
-  tiled_kernel<false><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
+  tiled_kernel<kDown><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(act), act_ld, offsets, counts, nullptr, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
+  return hipGetLastError();
+}
+
+}  // namespace lbmoe
+
+namespace lbmoe {
+
+bool tiled_router_supported(int E, int H) { return H % kBK == 0 && E >= 1; }
+
+hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
+                                      void* logits, hipStream_t s) {
+  GroupWeights gw{};
+  gw.gate_up = wg;
+  gw.E = E;
+  gw.H = H;
+  const int n_wtiles = (E + kWM - 1) / kWM;
+  const int64_t n_ttiles = (T + kWT - 1) / kWT;
+  tiled_kernel<kRouter><<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), H, nullptr, nullptr, nullptr, nullptr, 0, n_wtiles,
+      static_cast<int>(T), static_cast<uint16_t*>(logits), E);
   return hipGetLastError();
 }
 

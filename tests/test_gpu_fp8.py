@@ -86,6 +86,12 @@ def test_fp8_block_shared(gpu):
     _run_fp8(MoEShape(1024, 32, 4, 256, 512), 96, gpu, seed=5)
 
 
+@pytest.mark.parametrize("T", [2048, 3001])
+def test_fp8_block_prefill_tiled(gpu, T):
+    """Prefill-sized batch: fp8 LDS-tiled GEMMs (shared expert included)."""
+    _run_fp8(MoEShape(1024, 16, 2, 512, 256), T, gpu, seed=T, sample=64)
+
+
 def test_fp8_dense_mlp(gpu):
     shape = MoEShape(1024, 8, 2, 256, 512)
     w, g = make_layer(shape, seed=6)
