@@ -1,0 +1,152 @@
+"""The C ABI on the CPU: library loads, exports every declared entry point, struct layout
+matches the header, and host-side validation returns the documented status codes without
+touching a device."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from layerbatch_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lbmoe.h")
+
+OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_WORKSPACE = 0, -1, -2, -3, -4
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(lbmoe_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_entry_point(lbmoe):
+    names = declared_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lbmoe, n), n
+    assert set(names) == set(_lib.EXPORTED), "ctypes signatures out of sync with the header"
+    assert lbmoe.lbmoe_abi_version() == 1
+
+
+def test_struct_layout_matches_header(tmp_path):
+    fields = [f for f, _ in _lib.LbmoeLayer._fields_]
+    src = tmp_path / "probe.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
+             "int main(void) {", '  printf("%zu\\n", sizeof(lbmoe_layer));']
+    lines += [f'  printf("%zu\\n", offsetof(lbmoe_layer, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                           check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(_lib.LbmoeLayer)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(_lib.LbmoeLayer, f).offset == off, f
+
+
+def _layer(**kw):
+    L = _lib.LbmoeLayer()
+    L.hidden_size, L.num_experts, L.top_k = 2048, 128, 8
+    L.moe_intermediate_size, L.shared_intermediate_size = 768, 0
+    L.gate_weight, L.gate_up_proj, L.down_proj = 0x1000, 0x2000, 0x3000
+    for k, v in kw.items():
+        setattr(L, k, v)
+    return L
+
+
+@pytest.mark.parametrize("kw,status", [
+    ({}, OK),
+    ({"hidden_size": 1000}, ERR_SHAPE),
+    ({"num_experts": 0}, ERR_SHAPE),
+    ({"num_experts": 1025}, ERR_SHAPE),
+    ({"top_k": 0}, ERR_SHAPE),
+    ({"top_k": 129}, ERR_SHAPE),
+    ({"moe_intermediate_size": 100}, ERR_SHAPE),
+    ({"shared_intermediate_size": 64}, ERR_SHAPE),
+    ({"weight_dtype": 7}, ERR_DTYPE),
+    ({"gate_up_proj": None}, ERR_NULL),
+    ({"gate_weight": None}, ERR_NULL),
+    ({"shared_intermediate_size": 512}, ERR_NULL),          # shared weights missing
+    ({"weight_dtype": 1}, ERR_NULL),                        # fp8 scales missing
+    ({"weight_dtype": 1, "moe_intermediate_size": 640}, ERR_SHAPE),
+])
+def test_check_layer(lbmoe, kw, status):
+    L = _layer(**kw)
+    assert lbmoe.lbmoe_check_layer(ctypes.byref(L)) == status
+    assert lbmoe.lbmoe_check_layer(None) == ERR_NULL
+
+
+def test_workspace_size_arithmetic(lbmoe):
+    L = _layer()
+    sizes = []
+    for T in (0, 1, 128, 8192):
+        n = ctypes.c_size_t(0)
+        assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), T, ctypes.byref(n)) == OK
+        sizes.append(n.value)
+        assert n.value % 256 == 0
+    assert sizes == sorted(sizes) and sizes[-1] > sizes[1] > 0
+    n = ctypes.c_size_t(0)
+    # the expert outputs alone need T*k rows of H bf16
+    lbmoe.lbmoe_workspace_size(ctypes.byref(L), 128, ctypes.byref(n))
+    assert n.value >= 128 * 8 * 2048 * 2
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), -1, ctypes.byref(n)) == ERR_SHAPE
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), 1 << 22, ctypes.byref(n)) == ERR_SHAPE
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), 4, None) == ERR_NULL
+
+
+def test_workspace_regions_are_disjoint(lbmoe):
+    L = _layer(shared_intermediate_size=512, shared_gate_proj=1, shared_up_proj=1,
+               shared_down_proj=1, shared_expert_gate=1)
+    n = ctypes.c_size_t(0)
+    lbmoe.lbmoe_workspace_size(ctypes.byref(L), 300, ctypes.byref(n))
+    spans = [_lib.workspace_region(L, 300, r) for r in _lib.REGIONS]
+    spans.sort()
+    for (o0, b0), (o1, _) in zip(spans, spans[1:]):
+        assert o0 + b0 <= o1
+    assert spans[-1][0] + spans[-1][1] <= n.value
+    assert _lib.workspace_region(L, 300, "expert_out")[1] == (300 * 8 + 300) * 2048 * 2
+
+
+def test_forward_rejects_bad_arguments_before_any_device_call(lbmoe):
+    L = _layer()
+    n = ctypes.c_size_t(0)
+    lbmoe.lbmoe_workspace_size(ctypes.byref(L), 16, ctypes.byref(n))
+    p = ctypes.c_void_p(0x10000)
+    # T = 0 is a no-op
+    assert lbmoe.lbmoe_forward(ctypes.byref(L), None, 0, None, None, 0, None) == OK
+    assert lbmoe.lbmoe_forward(ctypes.byref(L), None, 16, p, p, n.value, None) == ERR_NULL
+    assert lbmoe.lbmoe_forward(ctypes.byref(L), p, 16, p, p, n.value - 1, None) == ERR_WORKSPACE
+    assert lbmoe.lbmoe_forward(ctypes.byref(_layer(top_k=0)), p, 16, p, p, n.value, None) == ERR_SHAPE
+    assert lbmoe.lbmoe_route(ctypes.byref(L), p, None, 4, p, 2, p, None, None) == ERR_DTYPE
+    assert lbmoe.lbmoe_route(ctypes.byref(L), p, None, 4, p, 4, p, ctypes.cast(p, ctypes.c_void_p), None) == ERR_NULL
+    assert lbmoe.lbmoe_permute(p, 3, 4, 2, 16, p, p, p, p, p, None, 0, None) == ERR_DTYPE
+    assert lbmoe.lbmoe_permute(p, 4, 4, 17, 16, p, p, p, p, p, None, 0, None) == ERR_SHAPE
+    assert lbmoe.lbmoe_permute(p, 4, 600, 8, 16, p, p, p, p, p, None, 0, None) == ERR_WORKSPACE
+    assert lbmoe.lbmoe_quantize_fp8_blocks(p, 2, 100, 128, p, p, None) == ERR_SHAPE
+    assert lbmoe.lbmoe_quantize_fp8_blocks(None, 2, 128, 128, p, p, None) == ERR_NULL
+    assert lbmoe.lbmoe_dense_mlp(p, p, p, None, None, None, 1024, 0, 0, p, 4, p, p, 1 << 20, None) == ERR_SHAPE
+
+
+def test_status_strings(lbmoe):
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        s = lbmoe.lbmoe_status_string(code).decode()
+        assert s and s != "unknown status"
+    assert lbmoe.lbmoe_status_string(42).decode() == "unknown status"
+
+
+def test_modules_refuse_cpu_tensors():
+    import torch
+    from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
+    blk = Qwen3_5SparseMoeBlock(256, 4, 2, 256, 0).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="gfx950 GPU"):
+        blk(torch.zeros((3, 256), dtype=torch.bfloat16))
+    # parameter names and shapes are the reference's (qwen3_5.py:765, :795-800, :894-897)
+    names = {k: tuple(v.shape) for k, v in Qwen3_5SparseMoeBlock(256, 4, 2, 256, 128).state_dict().items()}
+    assert names == {
+        "gate.weight": (4, 256), "experts.gate_up_proj": (4, 512, 256),
+        "experts.down_proj": (4, 256, 256), "shared_expert.gate_proj.weight": (128, 256),
+        "shared_expert.up_proj.weight": (128, 256), "shared_expert.down_proj.weight": (256, 128),
+        "shared_expert_gate.weight": (1, 256)}
