@@ -44,6 +44,9 @@ def parse():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="also run a plain copy kernel (torch.neg, fp32) over this many MiB, "
+                        "3 times: the calibration dispatch for FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
 
 
@@ -228,6 +231,15 @@ def main():
             "gate_up_tflops": round(pgf / (pgu * 1e-6) / 1e12, 2),
         }
         del pblk, px
+
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 18
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     out = {
         "metric": METRIC, "value": round(layer_gbs, 2), "unit": "GB/s", "n_gpus": 1,

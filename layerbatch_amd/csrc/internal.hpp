@@ -75,11 +75,14 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,
                           void* y, hipStream_t s);
-// LDS-tiled grouped GEMMs (prefill-sized batches).
-int tiled_max_tiles(int64_t rows, int groups);   // rows = routed + shared rows
+// LDS-tiled grouped GEMMs (prefill-sized batches). The bf16 kernels take a tile list of
+// wide and narrow token tiles, the fp8 kernels one of kFp8TileTokens-token tiles.
+enum TileListKind { kTilesBf16 = 0, kTilesFp8 = 1 };
+constexpr int kFp8TileTokens = 128;
+int tiled_max_tiles(int64_t rows, int groups, TileListKind kind);  // rows = routed + shared
 bool tiled_supported(const GroupWeights& gw);
 hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
-                              int32_t* tiles, hipStream_t s);
+                              TileListKind kind, int32_t* tiles, hipStream_t s);
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
                                 const int32_t* offsets, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,

@@ -37,10 +37,17 @@ __device__ __forceinline__ void wait_ring(int later) {
   }
 }
 
-// Workgroup b of a grid of nblk (a multiple of 8) runs on XCD b % 8; consecutive logical
-// indices are given to the same XCD so that tiles sharing operands share its L2.
-__device__ __forceinline__ int xcd_logical_block(int b, int nblk) {
-  return (b % 8) * (nblk / 8) + b / 8;
+// Workgroup b runs on XCD b % 8. The first `items` work items are spread over the 8 XCDs in
+// contiguous chunks, so consecutive items (which share operands) run together on one XCD's L2
+// and every XCD gets an equal share however much larger than `items` the grid is. Returns the
+// item of workgroup b, or -1 when b has none. The grid must hold at least round8(items)
+// workgroups.
+__device__ __forceinline__ int xcd_item(int b, int items) {
+  const int chunk = (items + 7) >> 3;
+  const int j = b >> 3;
+  if (j >= chunk) return -1;
+  const int item = (b & 7) * chunk + j;
+  return item < items ? item : -1;
 }
 
 inline unsigned round8(int64_t v) { return static_cast<unsigned>((v + 7) / 8 * 8); }

@@ -20,7 +20,7 @@ namespace f8t {
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kWM = 256;                 // weight rows per workgroup
-constexpr int kWT = 128;                 // tokens per workgroup (the shared tile list's width)
+constexpr int kWT = kFp8TileTokens;     // tokens per workgroup (the fp8 tile list's width)
 constexpr int kBK = 128;                 // k (= bytes) per LDS stage
 constexpr int kStages = 3;
 constexpr int kWaves = 4;
@@ -46,9 +46,9 @@ __global__ __launch_bounds__(256) void tiled_fp8_kernel(
     const int32_t* __restrict__ perm_tok, const int32_t* __restrict__ tiles, int max_tiles,
     int n_wtiles, int T, uint16_t* __restrict__ dst, int dst_ld) {
   __shared__ u32x4 lds[kStages][kStageU4];
-  const int logical = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int logical = xcd_item(blockIdx.x, tiles[2 * max_tiles] * n_wtiles);
+  if (logical < 0) return;
   const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  if (ti >= tiles[2 * max_tiles]) return;
   const int g = tiles[2 * ti], r0 = tiles[2 * ti + 1];
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;

@@ -1,23 +1,31 @@
 // LDS-tiled grouped GEMMs for prefill-sized batches (gfx950, v_mfma_f32_32x32x16_bf16).
 //
 // Same products as the streaming kernels (gate_up + SiLU*mul, qwen3_5.py:835-836; down,
-// qwen3_5.py:837), for groups with many tokens: a workgroup multiplies a tile of kWM weight
-// rows by a tile of kWT tokens of one expert, staging both operands through LDS in k-tiles of
-// kBK, so each operand byte fetched from L2 feeds kWT (or kWM) MFMA columns. The k-tiles move
-// global -> LDS directly (global_load_lds_dwordx4, no register staging) through a ring of
-// kStages buffers, loads running kStages-1 tiles ahead of the MFMAs.
+// qwen3_5.py:837), for groups with many tokens: a workgroup of 4 waves (2 x 2) multiplies a
+// tile of kWM = 256 weight rows by a tile of tokens of one expert, staging both operands
+// through LDS in k-tiles, so each operand byte fetched from L2 feeds many MFMA columns. The
+// k-tiles move global -> LDS directly (global_load_lds_dwordx4, no register staging) through
+// a ring of LDS buffers that is filled kStages k-tiles ahead of the MFMAs.
 //
-// Work list. build_tiles turns the per-expert token counts into a list of (group, first row)
-// token tiles; a launch covers max_tiles x n_tiles workgroups (a function of T only) and
-// workgroups past the list's end exit. Consecutive workgroups of one XCD take consecutive
-// (token tile, weight tile) pairs, weight tile fastest, so the tiles that share a token tile
-// run together on one XCD's L2.
+// Two token-tile widths share one launch. A wide tile (256 tokens, each wave 128 x 128) moves
+// the fewest operand bytes per flop, which matters here: with the whole chip busy the shader
+// clock settles near 1.5 GHz and every byte moved between L2 and LDS costs cycles and power.
+// A narrow tile (64 tokens, each wave 128 x 32) serves the few tokens that small experts get
+// under a skewed router: such a tile is bound by streaming the expert's weights from HBM, and
+// a wide tile would spend 4x the MFMA work on padding. Because the tile list follows expert
+// order, narrow (HBM-bound) and wide (MFMA-bound) tiles run side by side.
+//
+// Work list. build_tiles turns the per-expert token counts into a list of (group, first row |
+// narrow flag) token tiles; a launch covers max_tiles x n_wtiles workgroups (a function of T
+// only); the valid (token tile, weight tile) pairs, weight tile fastest, are dealt to the 8
+// XCDs in equal contiguous chunks (xcd_item) so that the tiles sharing a token tile run
+// together on one XCD's L2, and workgroups beyond the valid pairs exit.
 //
 // Layout. A = weight rows (MFMA rows), B = tokens (MFMA columns). Accumulator lane l of a
 // 32x32 tile holds token column l%32 and weight rows 8(v/4) + 4(l/32) + v%4, v = 0..15, so
-// four consecutive output channels of one token are stored together. LDS rows are kBK bf16
-// (64 bytes) in 16-byte chunks; chunk j of row r is stored at chunk j ^ ((r >> 2) & 3), which
-// keeps the 32-row MFMA operand reads free of bank conflicts.
+// four consecutive output channels of one token are stored together. LDS rows are kBK bf16 in
+// 16-byte chunks; chunk j of row r is stored at a row-dependent XOR of j (swz), which keeps
+// the 32-row MFMA operand reads free of bank conflicts.
 // Gate_up workgroups take kWM/2 channels: wave row-half h holds gate rows then up rows of the
 // same kWM/4 channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
@@ -26,67 +34,85 @@
 
 namespace lbmoe {
 
-// Tile configuration: kWavesM x kWavesN waves per workgroup, each wave owning kMT x kNT
-// 32x32 MFMA tiles (weights x tokens).
-#ifndef LBMOE_TILE_WAVES_N
-#define LBMOE_TILE_WAVES_N 1
-#endif
-#ifndef LBMOE_TILE_NT
-#define LBMOE_TILE_NT 4
-#endif
-#ifndef LBMOE_TILE_WPE
-#define LBMOE_TILE_WPE 1
-#endif
-constexpr int kWavesM = 2;
-constexpr int kWavesN = LBMOE_TILE_WAVES_N;
-constexpr int kMT = 4;                              // 32-row MFMA tiles per wave (weights)
-constexpr int kNT = LBMOE_TILE_NT;                  // 32-column MFMA tiles per wave (tokens)
+constexpr int kWavesM = 2;                          // waves along the weight rows
+constexpr int kWavesN = 2;                          // waves along the tokens
 constexpr int kWaves = kWavesM * kWavesN;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kMT = 4;                              // 32-row MFMA tiles per wave (weights)
 constexpr int kWM = kWavesM * kMT * 32;             // weight rows per workgroup
-constexpr int kWT = kWavesN * kNT * 32;             // tokens per workgroup
-#ifndef LBMOE_TILE_BK
-#define LBMOE_TILE_BK 32
-#endif
-constexpr int kBK = LBMOE_TILE_BK;                  // k per LDS stage
-#ifndef LBMOE_TILE_STAGES
-#define LBMOE_TILE_STAGES 3
-#endif
-constexpr int kStages = LBMOE_TILE_STAGES;          // LDS ring depth
-constexpr int kChunks = kBK / 8;                    // 16-byte chunks per LDS row
-constexpr int kRowsPerLoad = 64 / kChunks;          // rows one wave load covers
-constexpr int kALoads = kWM / kRowsPerLoad / kWaves;   // wave loads per stage (weights)
-constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;   // wave loads per stage (tokens)
-constexpr int kStageU4 = (kWM + kWT) * kChunks;     // 16-byte slots per stage
-static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
-              "loads must tile the stage");
 
-constexpr int kKSteps = kBK / 16;                  // MFMA k-steps per stage
-// Chunk j of LDS row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
-// kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
-constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
-static_assert(kChunks == 4 || kChunks == 8, "kBK must be 32 or 64");
-__device__ __forceinline__ int swz(int r, int j) {
-  return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
-}
+#ifndef LBMOE_TILE_BK
+#define LBMOE_TILE_BK 64
+#endif
+#ifndef LBMOE_TILE_STAGES
+#define LBMOE_TILE_STAGES 2
+#endif
+#ifndef LBMOE_NARROW_BK
+#define LBMOE_NARROW_BK 64
+#endif
+#ifndef LBMOE_NARROW_STAGES
+#define LBMOE_NARROW_STAGES 3
+#endif
+
+// One token-tile shape: NT 32-column MFMA tiles per wave, k-tiles of BK, STAGES LDS buffers.
+template <int NT, int BK, int STAGES>
+struct TileShape {
+  static constexpr int kNT = NT;
+  static constexpr int kWT = kWavesN * NT * 32;               // tokens per workgroup
+  static constexpr int kBK = BK;
+  static constexpr int kStages = STAGES;
+  static constexpr int kChunks = BK / 8;                      // 16-byte chunks per LDS row
+  static constexpr int kRowsPerLoad = 64 / kChunks;           // rows one wave copy covers
+  static constexpr int kALoads = kWM / kRowsPerLoad / kWaves;  // wave copies per stage (weights)
+  static constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;  // wave copies per stage (tokens)
+  static constexpr int kLoads = kALoads + kBLoads;
+  static constexpr int kStageU4 = (kWM + kWT) * kChunks;      // 16-byte slots per stage
+  static constexpr int kKSteps = BK / 16;                     // MFMA k-steps per k-tile
+  // Chunk j of row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
+  // kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
+  static constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
+  static_assert(kChunks == 4 || kChunks == 8, "BK must be 32 or 64");
+  static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
+                "copies must tile the stage");
+  static_assert(kKSteps % 2 == 0, "the next k-tile's first fragments go to register buffer 0");
+  static __device__ __forceinline__ int swz(int r, int j) {
+    return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
+  }
+};
+using Wide = TileShape<4, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
+using Narrow = TileShape<1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
+constexpr int kLdsU4 = Wide::kStages * Wide::kStageU4 > Narrow::kStages * Narrow::kStageU4
+                           ? Wide::kStages * Wide::kStageU4
+                           : Narrow::kStages * Narrow::kStageU4;
+static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
+
+constexpr int32_t kNarrowFlag = 1 << 30;
 
 // ---- tile list -------------------------------------------------------------------------------
-// tiles[2i] = group, tiles[2i+1] = first row within the group, in group order;
-// tiles[2*max_tiles] = number of valid entries. Groups: routed experts 0..E-1 with counts[g]
-// rows, then the shared expert (T rows) when present.
+// tiles[2i] = group, tiles[2i+1] = first row within the group (| kNarrowFlag for a narrow
+// tile), in group order; tiles[2*max_tiles] = number of valid entries. Groups: routed experts
+// 0..E-1 with counts[g] rows, then the shared expert (T rows) when present. A group of n rows
+// gets n / wide wide tiles; the remainder r is one more wide tile when r > wide - narrow (or
+// when narrow == 0), else ceil(r / narrow) narrow tiles.
+__device__ __forceinline__ int group_tiles(int n, int wide, int narrow, int& n_wide) {
+  n_wide = n / wide;
+  const int r = n - n_wide * wide;
+  if (r == 0) return n_wide;
+  if (narrow == 0 || r > wide - narrow) return ++n_wide;
+  return n_wide + (r + narrow - 1) / narrow;
+}
+
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
                                                            int E, int shared, int T, int max_tiles,
+                                                           int wide, int narrow,
                                                            int32_t* __restrict__ tiles) {
   __shared__ int wsum[16];
   const int G = E + shared;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (G + 1023) / 1024;
   const int lo = min(G, tid * per), hi = min(G, lo + per);
-  int local = 0;
-  for (int g = lo; g < hi; ++g) {
-    const int n = g < E ? counts[g] : T;
-    local += (n + kWT - 1) / kWT;
-  }
+  int local = 0, nw;
+  for (int g = lo; g < hi; ++g) local += group_tiles(g < E ? counts[g] : T, wide, narrow, nw);
   int incl = local;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -108,62 +134,49 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   int pos = incl - local + (wave > 0 ? wsum[wave - 1] : 0);
   for (int g = lo; g < hi; ++g) {
     const int n = g < E ? counts[g] : T;
-    for (int r = 0; r < n; r += kWT) {
+    const int nt = group_tiles(n, wide, narrow, nw);
+    for (int i = 0; i < nt; ++i, ++pos) {
       if (pos < max_tiles) {
         tiles[2 * pos] = g;
-        tiles[2 * pos + 1] = r;
+        tiles[2 * pos + 1] =
+            i < nw ? i * wide : (nw * wide + (i - nw) * narrow) | kNarrowFlag;
       }
-      ++pos;
     }
   }
   if (tid == 0) tiles[2 * max_tiles] = min(wsum[15], max_tiles);
 }
 
-// ---- the tiled kernel ----------------------------------------------------------------------
+// ---- one token tile --------------------------------------------------------------------------
 // MODE kDown: out[row, h] = act[row] . Wd_g[h];  kGateUp: act[row, c] = silu(gate) * up;
-// kRouter: logits[t, e] = x[t] . Wg[e] over token tiles t0 = 128 * tile (no tile list;
-// gw.gate_up holds the router weight, gw.E its row count).
+// kRouter: logits[t, e] = x[t] . Wg[e] (gw.gate_up holds the router weight, gw.E its rows).
 enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_TILE_WPE, LBMOE_TILE_WPE))) void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src,
-                                                    int src_ld, const int32_t* __restrict__ offsets,
-                                                    const int32_t* __restrict__ counts,
-                                                    const int32_t* __restrict__ perm_tok,
-                                                    const int32_t* __restrict__ tiles,
-                                                    int max_tiles, int n_wtiles, int T,
-                                                    uint16_t* __restrict__ dst, int dst_ld) {
+// Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
+// expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
+// src (down) / dst.
+template <int MODE, class S>
+__device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint16_t* __restrict__ src,
+                                             int src_ld, const int32_t* __restrict__ perm_tok,
+                                             int g, int r0, int n, int row0, int wt,
+                                             uint16_t* __restrict__ dst, int dst_ld,
+                                             u32x4* __restrict__ lds) {
   constexpr bool GATEUP = MODE == kGateUp, ROUTER = MODE == kRouter;
-  __shared__ u32x4 lds[kStages][kStageU4];
-  // XCD-aware order: hardware hands out workgroup b to XCD b % 8.
-  const int logical = xcd_logical_block(blockIdx.x, gridDim.x);
-  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  int g = 0, r0, n, row0;
-  if (ROUTER) {
-    if (ti * kWT >= T) return;
-    r0 = ti * kWT;
-    n = T;
-    row0 = 0;
-  } else {
-    if (ti >= tiles[2 * max_tiles]) return;
-    g = tiles[2 * ti];
-    r0 = tiles[2 * ti + 1];
-  }
+  constexpr int kNT = S::kNT, kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
+  constexpr int kRowsPerLoad = S::kRowsPerLoad, kALoads = S::kALoads, kBLoads = S::kBLoads;
+  constexpr int kLoads = S::kLoads, kKSteps = S::kKSteps, kStageU4 = S::kStageU4;
+  constexpr int kSwzShift = S::kSwzShift;
   const bool shared = !ROUTER && g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int H = gw.H;
-  if (!ROUTER) {
-    n = shared ? T : counts[g];
-    row0 = shared ? gw.sh_row0 : offsets[g];
-  }
   const int K = (GATEUP || ROUTER) ? H : Ig;
   const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel / output column
-  if (c0 >= (GATEUP ? Ig : (ROUTER ? gw.E : H))) return;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // Wave index as a scalar: LDS destinations of the copies (M0) are then computed on the SALU.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = w % kWavesM, wn = w / kWavesM;
 
-  // Direct global->LDS loads: wave load i writes one contiguous 1 KB LDS block of
+  // Direct global->LDS copies: wave copy i writes one contiguous 1 KB LDS block of
   // kRowsPerLoad rows; lane l fills slot l of it, i.e. row R0 + l/kChunks at swizzled position
   // l%kChunks, so it fetches the chunk that the swizzle places there.
   const uint16_t* wbase;
@@ -222,7 +235,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
   auto issue = [&](int stage, int k0) {
-    u32x4* buf = lds[stage];
+    u32x4* buf = lds + stage * kStageU4;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
       __builtin_amdgcn_global_load_lds(ap[i] + k0,
@@ -235,50 +248,87 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
                                        16, 0, 0);
   };
 
+  // Ring protocol. All kStages buffers are filled up front. In k-tile kt, once this wave
+  // has read the last k-step's fragments of stage kt, it waits for its copies of stage kt+1,
+  // meets the other waves at the barrier (after which nobody reads stage kt any more), reads
+  // stage kt+1's first fragments and refills stage kt's buffer with k-tile kt+kStages, all
+  // interleaved with the last k-step's MFMAs, so neither the copy issue nor the LDS read
+  // latency of the next k-tile stands between two MFMAs.
   const int nk = K / kBK;
 #pragma unroll
-  for (int st = 0; st < kStages - 1; ++st)
+  for (int st = 0; st < kStages; ++st)
     if (st < nk) issue(st, st * kBK);
   const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
   auto read_frags = [&](const u32x4* cur, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
     const int j = 2 * ks + mk;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) fa[i] = cur[swz(wm * (kWM / 2) + 32 * i + mr, j)];
+    for (int i = 0; i < kMT; ++i) fa[i] = cur[S::swz(wm * (kWM / 2) + 32 * i + mr, j)];
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) fb[t] = cur[swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
+    for (int t = 0; t < kNT; ++t) fb[t] = cur[S::swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
   };
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_ring<kStages - 2, kALoads + kBLoads>(nk - 1 - kt);
-    ring_barrier();
-    if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, (kt + kStages - 1) * kBK);
-    const u32x4* cur = lds[kt % kStages];
-    u32x4 fa[2][kMT], fb[2][kNT];
-    read_frags(cur, 0, fa[0], fb[0]);
+  auto mfma_all = [&](const u32x4 (&fa)[kMT], const u32x4 (&fb)[kNT]) {
 #pragma unroll
-    for (int ks = 0; ks < kKSteps; ++ks) {
-      if (ks + 1 < kKSteps) read_frags(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+    for (int i = 0; i < kMT; ++i)
 #pragma unroll
-      for (int i = 0; i < kMT; ++i)
+      for (int t = 0; t < kNT; ++t)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa[i]), as_bf16x8(fb[t]),
+                                                            acc[i][t], 0, 0, 0);
+  };
+  constexpr int kReads = kMT + kNT, kMfmas = kMT * kNT;
+  constexpr int kPaired = kReads < kMfmas ? kReads : kMfmas;
+  // fragment reads one-for-one with the first MFMAs (leftover reads after them)
+  auto sched_reads = [&]() {
 #pragma unroll
-        for (int t = 0; t < kNT; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(fa[ks & 1][i]),
-                                                              as_bf16x8(fb[ks & 1][t]),
-                                                              acc[i][t], 0, 0, 0);
+    for (int r = 0; r < kPaired; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    // Schedule: the first k-step's fragment reads, then each later k-step's reads
-    // interleaved one-for-one with the previous k-step's MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, kMT + kNT, 0);
+    if constexpr (kReads > kPaired) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPaired, 0);
+  };
+  u32x4 fa[2][kMT], fb[2][kNT];
+  // One k-tile. NEXT: a k-tile follows (wait, barrier, read its first fragments); REFILL: the
+  // freed buffer takes k-tile kt + kStages. Specialised at compile time so that the loop body
+  // has no branches around the MFMAs.
+  auto ktile = [&]<bool NEXT, bool REFILL>(int kt) {
+    const u32x4* cur = lds + (kt % kStages) * kStageU4;
 #pragma unroll
     for (int ks = 0; ks + 1 < kKSteps; ++ks) {
-#pragma unroll
-      for (int r = 0; r < kMT + kNT; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT - (kMT + kNT), 0);
+      read_frags(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      mfma_all(fa[ks & 1], fb[ks & 1]);
+      sched_reads();
+      if constexpr (kMfmas > kPaired) __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPaired, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT, 0);
-  }
+    constexpr int kl = (kKSteps - 1) & 1;
+    if constexpr (NEXT) {
+      // all earlier MFMAs stay above the barrier: they cover the last fragment reads' latency
+      __builtin_amdgcn_sched_barrier(0);
+      wait_ring<kStages - 2, kLoads>(nk - 2 - kt);
+      ring_barrier();
+      read_frags(lds + ((kt + 1) % kStages) * kStageU4, 0, fa[0], fb[0]);
+      if constexpr (REFILL) issue(kt % kStages, (kt + kStages) * kBK);
+    }
+    mfma_all(fa[kl], fb[kl]);
+    if constexpr (NEXT) {
+      // next k-tile's first reads with the first MFMAs, then the copies spread over the rest
+      sched_reads();
+      constexpr int kRest = kMfmas - kPaired;
+      if constexpr (REFILL && kRest > 0) {
+        constexpr int kPer = (kLoads + kRest - 1) / (kRest > 0 ? kRest : 1);
+#pragma unroll
+        for (int r = 0; r < kRest; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, kPer, 0);
+        }
+      }
+    }
+  };
+  wait_ring<kStages - 1, kLoads>(nk - 1);
+  ring_barrier();
+  read_frags(lds, 0, fa[0], fb[0]);
+  int kt = 0;
+  for (; kt + kStages < nk; ++kt) ktile.template operator()<true, true>(kt);
+  for (; kt + 1 < nk; ++kt) ktile.template operator()<true, false>(kt);
+  ktile.template operator()<false, false>(kt);
 
   // Epilogue.
   const int col = lane & 31, rq = 4 * (lane >> 5);
@@ -330,23 +380,75 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(LBMOE_
   }
 }
 
-// Upper bound of the token-tile count: every group adds at most one partial tile.
-int tiled_max_tiles(int64_t rows, int groups) {
-  return static_cast<int>((rows + kWT - 1) / kWT) + groups + 1;
+// ---- the kernels -----------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
+                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ counts,
+                  const int32_t* __restrict__ perm_tok, const int32_t* __restrict__ tiles,
+                  int max_tiles, int n_wtiles, int T, uint16_t* __restrict__ dst, int dst_ld) {
+  __shared__ u32x4 lds[kLdsU4];
+  if (MODE == kRouter) {
+    // token tiles of Narrow::kWT over all T tokens; no tile list
+    const int logical = xcd_item(blockIdx.x, (T + Narrow::kWT - 1) / Narrow::kWT * n_wtiles);
+    if (logical < 0) return;
+    const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
+    tile_product<MODE, Narrow>(gw, src, src_ld, nullptr, 0, ti * Narrow::kWT, T, 0, wt, dst,
+                               dst_ld, lds);
+    return;
+  }
+  // XCD-aware order over the valid (token tile, weight tile) pairs
+  const int logical = xcd_item(blockIdx.x, tiles[2 * max_tiles] * n_wtiles);
+  if (logical < 0) return;
+  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
+  const int g = tiles[2 * ti], e = tiles[2 * ti + 1];
+  const bool shared = g == gw.E;
+  if (wt * (MODE == kGateUp ? kWM / 2 : kWM) >= (MODE == kGateUp ? (shared ? gw.Is : gw.I) : gw.H))
+    return;
+  const int n = shared ? T : counts[g];
+  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  if (e & kNarrowFlag)
+    tile_product<MODE, Narrow>(gw, src, src_ld, perm_tok, g, e & (kNarrowFlag - 1), n, row0, wt,
+                               dst, dst_ld, lds);
+  else
+    tile_product<MODE, Wide>(gw, src, src_ld, perm_tok, g, e, n, row0, wt, dst, dst_ld, lds);
+}
+
+// ---- host side -------------------------------------------------------------------------------
+static void tile_widths(TileListKind kind, int& wide, int& narrow) {
+  if (kind == kTilesFp8) {
+    wide = kFp8TileTokens;
+    narrow = 0;
+  } else {
+    wide = Wide::kWT;
+    narrow = Narrow::kWT;
+  }
+}
+
+// Upper bound of the tile-list length: rows / wide full tiles, plus per group at most one
+// partial wide tile or (wide - narrow) / narrow narrow tiles.
+int tiled_max_tiles(int64_t rows, int groups, TileListKind kind) {
+  int wide, narrow;
+  tile_widths(kind, wide, narrow);
+  const int per_group = narrow == 0 ? 1 : (wide - narrow) / narrow;
+  return static_cast<int>(rows / wide) + groups * per_group + 1;
 }
 
 bool tiled_supported(const GroupWeights& gw) {
-  return gw.H % kWM == 0 && gw.H % kBK == 0 && gw.I % (kWM / 2) == 0 &&
-         (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBK == 0 && gw.I < (1 << 20);
+  constexpr int kBKmax = Wide::kBK > Narrow::kBK ? Wide::kBK : Narrow::kBK;
+  return gw.H % kWM == 0 && gw.H % kBKmax == 0 && gw.I % (kWM / 2) == 0 &&
+         (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBKmax == 0 &&
+         (gw.Is == 0 || gw.Is % kBKmax == 0) && gw.I < (1 << 20);
 }
 
 hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
-                              int32_t* tiles, hipStream_t s) {
+                              TileListKind kind, int32_t* tiles, hipStream_t s) {
+  int wide, narrow;
+  tile_widths(kind, wide, narrow);
   build_tiles_kernel<<<1, 1024, 0, s>>>(counts, E, shared ? 1 : 0, static_cast<int>(T), max_tiles,
-                                        tiles);
+                                        wide, narrow, tiles);
   return hipGetLastError();
 }
-
 
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
                                 const int32_t* offsets, const int32_t* perm_tok,
@@ -370,11 +472,7 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
   return hipGetLastError();
 }
 
-}  // namespace lbmoe
-
-namespace lbmoe {
-
-bool tiled_router_supported(int E, int H) { return H % kBK == 0 && E >= 1; }
+bool tiled_router_supported(int E, int H) { return H % Narrow::kBK == 0 && E >= 1; }
 
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s) {
@@ -383,7 +481,7 @@ hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, 
   gw.E = E;
   gw.H = H;
   const int n_wtiles = (E + kWM - 1) / kWM;
-  const int64_t n_ttiles = (T + kWT - 1) / kWT;
+  const int64_t n_ttiles = (T + Narrow::kWT - 1) / Narrow::kWT;
   tiled_kernel<kRouter><<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), H, nullptr, nullptr, nullptr, nullptr, 0, n_wtiles,
       static_cast<int>(T), static_cast<uint16_t*>(logits), E);
