@@ -156,6 +156,24 @@ def work(shape, T, n_hit):
     return layer_bytes, layer_flops, gu_bytes, gu_flops
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_decode_qwen3-30b-a3b_T128_pmc_traffic.txt")
+
+
+def pmc_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` at the default decode workload, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a copy kernel); None if the
+    summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 4 and parts[0] == kernel:
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(blk, x, zipf, budget_s):
     """The torch-CPU restatement of the reference path on this host's cores."""
     import torch
@@ -241,6 +259,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    default_workload = args.shape == "qwen3-30b-a3b" and args.T == 128
+    traffic = pmc_traffic("gate_up_bf16_kernel") if default_workload else None
+
     out = {
         "metric": METRIC, "value": round(layer_gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(d["wall_us"] / 1e3, 4),
@@ -257,7 +278,7 @@ def main():
         "stage_us": {k_: round(v, 2) for k_, v in d["stage_us"].items()},
         "roofline": {"kernel": "gate_up_bf16_kernel", "bound": "hbm", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": gb,
+                     "traffic": traffic, "algorithmic_bytes_per_launch": gb,
                      "avg_launch_us": round(gu_us, 2)},
         "cpu_baseline": cpu,
         "prefill": prefill,

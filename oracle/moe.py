@@ -39,6 +39,10 @@ tests/test_oracle.py and tests/test_golden.py):
   (oracle/torch_ref.py) within bf16 tolerance.
 * fp8 functions: quantise/dequantise round trips, exactness on e4m3-representable blocks,
   scale closed forms, and the bf16 oracle within fp8 error bounds.
+* the reference module itself: tests/golden/reference_moe_small.npz holds outputs recorded
+  from the reference's Qwen3_5SparseMoeBlock (tests/golden/make_reference_golden.py);
+  tests/test_golden.py checks torch_ref bit for bit against them and this oracle for
+  selection modulo boundary ties and outputs within 1e-2.
 """
 import numpy as np
 
