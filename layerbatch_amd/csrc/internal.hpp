@@ -9,7 +9,7 @@
 
 namespace lbmoe {
 
-// Permutations of at most kPermSingle entries run in one wave; larger ones in chunks of
+// Permutations of at most kPermSingle entries run in one workgroup; larger ones in chunks of
 // kPermChunk entries, one wave per chunk.
 constexpr int kPermSingle = 1024;
 constexpr int kPermChunk = 256;

@@ -13,7 +13,7 @@
 //   offsets   one workgroup: exclusive scan of the totals -> counts[e], offsets[e].
 //   scatter   one wave per chunk: pos = offsets[e] + base[e][chunk] + rank -> perm_tok,
 //             perm_slot, inv.
-// Up to kPermSingle entries (decode-sized batches) run all of it in a single one-wave kernel.
+// Up to kPermSingle entries (decode-sized batches) run all of it in a single workgroup.
 // Entries whose expert id lies outside [0, E) are left out of every list and get inv = -1.
 #include "common.hpp"
 #include "internal.hpp"
@@ -71,7 +71,6 @@ __device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E,
 }
 
 constexpr int kRounds = kPermChunk / kWave;
-constexpr int kSingleRounds = kPermSingle / kWave;
 
 template <int IB>
 __global__ __launch_bounds__(64) void perm_count(const void* idx, int T, int k, int E,
@@ -178,55 +177,71 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
   }
 }
 
-// Whole permutation in one wave when V <= kPermSingle (decode-sized batches).
+// Whole permutation in one workgroup when V <= kPermSingle (decode-sized batches): wave w
+// takes entries v = 64w .. 64w+63, ranks them among equal experts of the wave (ballot match),
+// and records the wave's count per expert; one thread per expert then turns the counts into
+// per-wave prefixes and a total, a block scan of the totals gives the offsets, and every
+// entry lands at offsets[e] + (entries of e in earlier waves) + rank.
 template <int IB>
-__global__ __launch_bounds__(64) void perm_single(const void* idx, int T, int k, int E,
-                                                  int nbits, int V, int32_t* counts,
-                                                  int32_t* offsets, int32_t* perm_tok,
-                                                  int32_t* perm_slot, int32_t* inv) {
-  __shared__ int run[1024];
+__global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int T, int k, int E,
+                                                           int nbits, int V, int32_t* counts,
+                                                           int32_t* offsets, int32_t* perm_tok,
+                                                           int32_t* perm_slot, int32_t* inv) {
+  constexpr int kW = kPermSingle / kWave;
+  __shared__ int cnt[kW][1024];          // per wave and expert: count, then exclusive prefix
   __shared__ int start[1024];
-  const int lane = lane_id();
-  for (int e = lane; e < E; e += kWave) run[e] = 0;
+  __shared__ int wsum[kW];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int i = tid; i < kW * 1024; i += kPermSingle) (&cnt[0][0])[i] = 0;
+  const int v = tid;
+  int e = -1, s = 0, t = 0;
+  if (v < V) {
+    s = v / T;
+    t = v - s * T;
+    e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
+  }
+  const bool valid = (e >= 0) && (e < E);
+  const uint64_t m = match_expert(valid ? e : 0, __ballot(valid), nbits);
+  const int rank = mask_rank(m);
   __syncthreads();
-  int ee[kSingleRounds], rk[kSingleRounds];
-  rank_chunk<IB, kSingleRounds>(idx, T, k, E, nbits, V, 0, run, ee, rk);
+  if (valid && rank == 0) cnt[wave][e] = __popcll(m);
   __syncthreads();
-  // exclusive scan of run[0..E) by one wave: each lane owns a contiguous slice
-  const int per = (E + kWave - 1) / kWave;
-  const int lo = min(E, lane * per), hi = min(E, lo + per);
-  int local = 0;
-  for (int e = lo; e < hi; ++e) local += run[e];
-  int incl = local;
+  int total = 0;
+  if (tid < E) {
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
+    for (int w = 0; w < kW; ++w) {
+      const int c = cnt[w][tid];
+      cnt[w][tid] = total;
+      total += c;
+    }
+  }
+  int incl = total;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
     const int y = __shfl_up(incl, o, kWave);
     if (lane >= o) incl += y;
   }
-  int acc = incl - local;
-  for (int e = lo; e < hi; ++e) {
-    start[e] = acc;
-    offsets[e] = acc;
-    counts[e] = run[e];
-    acc += run[e];
-  }
-  if (lane == 63) offsets[E] = incl;
+  if (lane == kWave - 1) wsum[wave] = incl;
   __syncthreads();
-#pragma unroll
-  for (int r = 0; r < kSingleRounds; ++r) {
-    const int v = r * kWave + lane;
-    if (v < V) {
-      const int s = v / T;
-      const int t = v - s * T;
-      const int64_t ts = static_cast<int64_t>(t) * k + s;
-      if (ee[r] < 0) {
-        inv[ts] = -1;
-      } else {
-        const int pos = start[ee[r]] + rk[r];
-        perm_tok[pos] = t;
-        perm_slot[pos] = s;
-        inv[ts] = pos;
-      }
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
+  const int excl = before + incl - total;
+  if (tid < E) {
+    start[tid] = excl;
+    counts[tid] = total;
+    offsets[tid] = excl;
+  }
+  if (tid == kPermSingle - 1) offsets[E] = before + incl;
+  __syncthreads();
+  if (v < V) {
+    const int64_t ts = static_cast<int64_t>(t) * k + s;
+    if (!valid) {
+      inv[ts] = -1;
+    } else {
+      const int pos = start[e] + cnt[wave][e] + rank;
+      perm_tok[pos] = t;
+      perm_slot[pos] = s;
+      inv[ts] = pos;
     }
   }
 }
@@ -256,8 +271,8 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
   const int V = static_cast<int>(T * k);
   const int nbits = bits_for(E);
   if (V <= kPermSingle) {
-    perm_single<IB><<<1, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, counts, offsets,
-                                     perm_tok, perm_slot, inv);
+    perm_single<IB><<<1, kPermSingle, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, counts,
+                                              offsets, perm_tok, perm_slot, inv);
     return hipGetLastError();
   }
   // hist, base: E x nblk; lrank: V; the totals reuse the counts array until perm_offsets
