@@ -332,24 +332,50 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 
   // Epilogue.
   const int col = lane & 31, rq = 4 * (lane >> 5);
+  if constexpr (!ROUTER) {
+    // Stage the tile in LDS as row-major [token][column] bf16, then store whole row segments
+    // (kCols * 2 contiguous bytes per token) with 16-byte lanes. Storing straight from the
+    // accumulators would write 16-byte pieces of 32 token rows per instruction. 16-byte chunk
+    // c of staged row r sits at chunk c ^ (r mod kRowChunks), which spreads the 32 rows of an
+    // accumulator write over distinct banks.
+    constexpr int kCols = GATEUP ? kWM / 2 : kWM;            // output columns per tile
+    constexpr int kRowChunks = kCols / 8;
+    static_assert(S::kWT * kRowChunks <= kLdsU4, "staged tile exceeds the LDS ring");
+    auto slot = [&](int r, int c) { return r * kRowChunks + (c ^ (r & (kRowChunks - 1))); };
+    __syncthreads();                                          // every wave is done with the ring
+    char* st = reinterpret_cast<char*>(lds);
 #pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    const int p = r0 + wn * (kNT * 32) + 32 * t + col;
-    if (p >= n) continue;
-    uint16_t* orow = dst + static_cast<int64_t>(row0 + p) * dst_ld;
-    if (GATEUP) {
+    for (int t = 0; t < kNT; ++t) {
+      const int r = wn * (kNT * 32) + 32 * t + col;           // token within the tile
 #pragma unroll
-      for (int i = 0; i < kMT / 2; ++i)
+      for (int i = 0; i < (GATEUP ? kMT / 2 : kMT); ++i)
 #pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) {
           float a[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            a[v] = silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v];
-          const int ch = c0 + wm * (kWM / 4) + 32 * i + 8 * v4 + rq;
-          *reinterpret_cast<u32x2*>(orow + ch) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+            a[v] = GATEUP ? silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v]
+                          : acc[i][t][4 * v4 + v];
+          const int c = (GATEUP ? wm * (kWM / 4) : wm * (kWM / 2)) + 32 * i + 8 * v4 + rq;
+          *reinterpret_cast<u32x2*>(st + slot(r, c / 8) * 16 + (c % 8) * 2) =
+              u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
-    } else if (ROUTER) {
+    }
+    __syncthreads();
+    constexpr int kRowsPerPass = kThreads / kRowChunks;
+    const int c = threadIdx.x % kRowChunks;
+    for (int r = threadIdx.x / kRowChunks; r < S::kWT; r += kRowsPerPass) {
+      const int p = r0 + r;
+      if (p >= n) break;
+      *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(row0 + p) * dst_ld + c0 + 8 * c) =
+          lds[slot(r, c)];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int p = r0 + wn * (kNT * 32) + 32 * t + col;
+      if (p >= n) continue;
+      uint16_t* orow = dst + static_cast<int64_t>(row0 + p) * dst_ld;
       const int E = gw.E;
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
@@ -365,16 +391,6 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
             for (int v = 0; v < 4; ++v)
               if (e + v < E) orow[e + v] = static_cast<uint16_t>(f2bf(acc[i][t][4 * v4 + v]));
           }
-        }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) {
-          const int h = c0 + wm * (kWM / 2) + 32 * i + 8 * v4 + rq;
-          *reinterpret_cast<u32x2*>(orow + h) =
-              u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
-                    pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
         }
     }
   }
