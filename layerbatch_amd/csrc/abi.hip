@@ -37,7 +37,7 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
   w.bytes[R_LRANK] = V * 4;
   const int64_t max_tiles = std::max(tiled_max_tiles(Vs, E + 1, kTilesBf16),
                                      tiled_max_tiles(Vs, E + 1, kTilesFp8));
-  w.bytes[R_TILES] = (2 * max_tiles + 1) * 4;
+  w.bytes[R_TILES] = (2 * max_tiles + kTileListTail) * 4;
   if (is_fp8(L)) {
     w.bytes[R_XQ] = T * H;
     w.bytes[R_XS] = T * (H / 128) * 4;

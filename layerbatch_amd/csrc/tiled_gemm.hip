@@ -16,10 +16,10 @@
 // order, narrow (HBM-bound) and wide (MFMA-bound) tiles run side by side.
 //
 // Work list. build_tiles turns the per-expert token counts into a list of (group, first row |
-// narrow flag) token tiles; a launch covers max_tiles x n_wtiles workgroups (a function of T
-// only); the valid (token tile, weight tile) pairs, weight tile fastest, are dealt to the 8
-// XCDs in equal contiguous chunks (xcd_item) so that the tiles sharing a token tile run
-// together on one XCD's L2, and workgroups beyond the valid pairs exit.
+// narrow flag) token tiles, wide ones first; a launch has one workgroup per possible
+// (token tile, weight tile) item (a function of T only), and dispatch_item maps workgroups to
+// items so that each XCD works on its own share, with small-expert tiles spread over the
+// launch and its last round.
 //
 // Layout. A = weight rows (MFMA rows), B = tokens (MFMA columns). Accumulator lane l of a
 // 32x32 tile holds token column l%32 and weight rows 8(v/4) + 4(l/32) + v%4, v = 0..15, so
@@ -90,16 +90,43 @@ constexpr int32_t kNarrowFlag = 1 << 30;
 
 // ---- tile list -------------------------------------------------------------------------------
 // tiles[2i] = group, tiles[2i+1] = first row within the group (| kNarrowFlag for a narrow
-// tile), in group order; tiles[2*max_tiles] = number of valid entries. Groups: routed experts
-// 0..E-1 with counts[g] rows, then the shared expert (T rows) when present. A group of n rows
-// gets n / wide wide tiles; the remainder r is one more wide tile when r > wide - narrow (or
-// when narrow == 0), else ceil(r / narrow) narrow tiles.
-__device__ __forceinline__ int group_tiles(int n, int wide, int narrow, int& n_wide) {
+// tile). All wide tiles come first, in group order, then all narrow tiles, in group order.
+// Behind the max_tiles entries: tiles[2*max_tiles] = number of valid entries,
+// tiles[2*max_tiles+1] = number of wide entries. Groups: routed experts 0..E-1 with counts[g]
+// rows, then the shared expert (T rows) when present. A group of n rows gets n / wide wide
+// tiles; the remainder r is one more wide tile when r > wide - narrow (or when narrow == 0),
+// else ceil(r / narrow) narrow tiles.
+__device__ __forceinline__ void group_tiles(int n, int wide, int narrow, int& n_wide,
+                                            int& n_narrow) {
   n_wide = n / wide;
+  n_narrow = 0;
   const int r = n - n_wide * wide;
-  if (r == 0) return n_wide;
-  if (narrow == 0 || r > wide - narrow) return ++n_wide;
-  return n_wide + (r + narrow - 1) / narrow;
+  if (r == 0) return;
+  if (narrow == 0 || r > wide - narrow) ++n_wide;
+  else n_narrow = (r + narrow - 1) / narrow;
+}
+
+// Block-wide exclusive scan of one int per thread (1024 threads); returns the total.
+__device__ __forceinline__ int block_scan_1024(int v, int& excl, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    const int c = wsum[w];
+    before += w < wave ? c : 0;
+    total += c;
+  }
+  excl = before + incl - v;
+  __syncthreads();
+  return total;
 }
 
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
@@ -108,42 +135,38 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ tiles) {
   __shared__ int wsum[16];
   const int G = E + shared;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int per = (G + 1023) / 1024;
   const int lo = min(G, tid * per), hi = min(G, lo + per);
-  int local = 0, nw;
-  for (int g = lo; g < hi; ++g) local += group_tiles(g < E ? counts[g] : T, wide, narrow, nw);
-  int incl = local;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < 16 ? wsum[lane] : 0;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const int y = __shfl_up(w, o, kWave);
-      if (lane >= o) w += y;
-    }
-    if (lane < 16) wsum[lane] = w;
-  }
-  __syncthreads();
-  int pos = incl - local + (wave > 0 ? wsum[wave - 1] : 0);
+  int lw = 0, ln = 0, nw, nn;
   for (int g = lo; g < hi; ++g) {
-    const int n = g < E ? counts[g] : T;
-    const int nt = group_tiles(n, wide, narrow, nw);
-    for (int i = 0; i < nt; ++i, ++pos) {
-      if (pos < max_tiles) {
-        tiles[2 * pos] = g;
-        tiles[2 * pos + 1] =
-            i < nw ? i * wide : (nw * wide + (i - nw) * narrow) | kNarrowFlag;
+    group_tiles(g < E ? counts[g] : T, wide, narrow, nw, nn);
+    lw += nw;
+    ln += nn;
+  }
+  int pw, pn;
+  const int tw = block_scan_1024(lw, pw, wsum);
+  const int tn = block_scan_1024(ln, pn, wsum);
+  pn += tw;
+  for (int g = lo; g < hi; ++g) {
+    group_tiles(g < E ? counts[g] : T, wide, narrow, nw, nn);
+    for (int i = 0; i < nw; ++i, ++pw) {
+      if (pw < max_tiles) {
+        tiles[2 * pw] = g;
+        tiles[2 * pw + 1] = i * wide;
+      }
+    }
+    for (int i = 0; i < nn; ++i, ++pn) {
+      if (pn < max_tiles) {
+        tiles[2 * pn] = g;
+        tiles[2 * pn + 1] = (nw * wide + i * narrow) | kNarrowFlag;
       }
     }
   }
-  if (tid == 0) tiles[2 * max_tiles] = min(wsum[15], max_tiles);
+  if (tid == 0) {
+    tiles[2 * max_tiles] = min(tw + tn, max_tiles);
+    tiles[2 * max_tiles + 1] = min(tw, max_tiles);
+  }
 }
 
 // ---- one token tile --------------------------------------------------------------------------
@@ -342,7 +365,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     constexpr int kRowChunks = kCols / 8;
     static_assert(S::kWT * kRowChunks <= kLdsU4, "staged tile exceeds the LDS ring");
     auto slot = [&](int r, int c) { return r * kRowChunks + (c ^ (r & (kRowChunks - 1))); };
-    __syncthreads();                                          // every wave is done with the ring
+    ring_barrier();                                           // every wave is done with the ring
     char* st = reinterpret_cast<char*>(lds);
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
@@ -361,7 +384,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
               u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
     }
-    __syncthreads();
+    ring_barrier();
     constexpr int kRowsPerPass = kThreads / kRowChunks;
     const int c = threadIdx.x % kRowChunks;
     for (int r = threadIdx.x / kRowChunks; r < S::kWT; r += kRowsPerPass) {
@@ -397,6 +420,42 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 }
 
 // ---- the kernels -----------------------------------------------------------------------------
+// Router logits: one workgroup per (token tile of Narrow::kWT, weight tile), no tile list.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T, int n_wtiles,
+                         uint16_t* __restrict__ logits) {
+  __shared__ u32x4 lds[kLdsU4];
+  const int logical = xcd_item(blockIdx.x, (T + Narrow::kWT - 1) / Narrow::kWT * n_wtiles);
+  if (logical < 0) return;
+  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
+  tile_product<kRouter, Narrow>(gw, x, gw.H, nullptr, 0, ti * Narrow::kWT, T, 0, wt, logits,
+                                gw.E, lds);
+}
+
+// Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
+// fastest; the W wide items come first, then the N narrow ones. XCD x owns the x-th contiguous
+// eighth of the wide items and of the narrow items, so items that share a token tile run on
+// one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
+// (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
+// (short, HBM-bound) items, so that the launch ends on short items, and its other narrow items
+// are spread evenly between the wide (MFMA-bound) ones, so that weight streaming for small
+// experts overlaps MFMA work. Returns the item of workgroup b, or -1.
+constexpr int kTailSlots = 32;
+__device__ __forceinline__ int dispatch_item(int b, int W, int N) {
+  const int x = b & 7, j = b >> 3;
+  const int cw = (W + 7) >> 3, cn = (N + 7) >> 3;
+  const int w0 = min(W, x * cw), nw = min(W, w0 + cw) - w0;     // this XCD's wide items
+  const int n0 = min(N, x * cn), nn = min(N, n0 + cn) - n0;     // and narrow items
+  if (j >= nw + nn) return -1;
+  const int tail = min(nn, kTailSlots);
+  const int spread = nn - tail, prefix = nw + spread;
+  if (j >= prefix) return W + n0 + spread + (j - prefix);       // the tail: narrow items
+  // narrow items before slot j in the prefix: floor(j * spread / prefix)
+  const int before = static_cast<int>(static_cast<int64_t>(j) * spread / prefix);
+  const int upto = static_cast<int>(static_cast<int64_t>(j + 1) * spread / prefix);
+  return upto > before ? W + n0 + before : w0 + (j - before);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
@@ -404,23 +463,14 @@ void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
                   const int32_t* __restrict__ perm_tok, const int32_t* __restrict__ tiles,
                   int max_tiles, int n_wtiles, int T, uint16_t* __restrict__ dst, int dst_ld) {
   __shared__ u32x4 lds[kLdsU4];
-  if (MODE == kRouter) {
-    // token tiles of Narrow::kWT over all T tokens; no tile list
-    const int logical = xcd_item(blockIdx.x, (T + Narrow::kWT - 1) / Narrow::kWT * n_wtiles);
-    if (logical < 0) return;
-    const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-    tile_product<MODE, Narrow>(gw, src, src_ld, nullptr, 0, ti * Narrow::kWT, T, 0, wt, dst,
-                               dst_ld, lds);
-    return;
-  }
-  // XCD-aware order over the valid (token tile, weight tile) pairs
-  const int logical = xcd_item(blockIdx.x, tiles[2 * max_tiles] * n_wtiles);
-  if (logical < 0) return;
-  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
+  const int n_all = tiles[2 * max_tiles], n_wide = tiles[2 * max_tiles + 1];
+  const int item = dispatch_item(blockIdx.x, n_wide * n_wtiles, (n_all - n_wide) * n_wtiles);
+  if (item < 0) return;
+  const int ti = item / n_wtiles, wt = item - ti * n_wtiles;
   const int g = tiles[2 * ti], e = tiles[2 * ti + 1];
   const bool shared = g == gw.E;
   if (wt * (MODE == kGateUp ? kWM / 2 : kWM) >= (MODE == kGateUp ? (shared ? gw.Is : gw.I) : gw.H))
-    return;
+    return;                                  // weight tile past a narrower shared expert
   const int n = shared ? T : counts[g];
   const int row0 = shared ? gw.sh_row0 : offsets[g];
   if (e & kNarrowFlag)
@@ -466,23 +516,28 @@ hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t
   return hipGetLastError();
 }
 
+// One workgroup per item; per-XCD rounding of the two item ranges adds at most 16 slots.
+static unsigned item_grid(int max_tiles, int n_wtiles) {
+  return round8(static_cast<int64_t>(max_tiles) * n_wtiles + 16);
+}
+
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
                                 const int32_t* offsets, const int32_t* perm_tok,
-                                const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
+                                int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s) {
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   const int n_wtiles = Imax / (kWM / 2);
-  tiled_kernel<kGateUp><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
+  tiled_kernel<kGateUp><<<item_grid(max_tiles, n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), gw.H, offsets, counts, perm_tok, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
 }
 
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
-                             const int32_t* counts, const int32_t* offsets, const int32_t* tiles,
+                             const int32_t* counts, const int32_t* offsets, int32_t* tiles,
                              int max_tiles, int64_t T, void* out, hipStream_t s) {
   const int n_wtiles = gw.H / kWM;
-  tiled_kernel<kDown><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), kThreads, 0, s>>>(
+  tiled_kernel<kDown><<<item_grid(max_tiles, n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(act), act_ld, offsets, counts, nullptr, tiles, max_tiles,
       n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
   return hipGetLastError();
@@ -498,9 +553,9 @@ hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, 
   gw.H = H;
   const int n_wtiles = (E + kWM - 1) / kWM;
   const int64_t n_ttiles = (T + Narrow::kWT - 1) / Narrow::kWT;
-  tiled_kernel<kRouter><<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(x), H, nullptr, nullptr, nullptr, nullptr, 0, n_wtiles,
-      static_cast<int>(T), static_cast<uint16_t*>(logits), E);
+  router_tiled_kernel<<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), static_cast<int>(T), n_wtiles,
+      static_cast<uint16_t*>(logits));
   return hipGetLastError();
 }
 
