@@ -82,16 +82,18 @@ constexpr int kFp8TileTokens = 128;
 // Words behind a tile list's entries: count, wide count.
 constexpr int kTileListTail = 2;
 int tiled_max_tiles(int64_t rows, int groups, TileListKind kind);  // rows = routed + shared
+// Bytes of a bf16 tile list with max_tiles entries and the dispatch tables of both GEMMs.
+int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H);
 bool tiled_supported(const GroupWeights& gw);
-hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
-                              TileListKind kind, int32_t* tiles, hipStream_t s);
-hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
-                                const int32_t* offsets, const int32_t* perm_tok,
-                                int32_t* tiles, int max_tiles, int64_t T, int act_ld,
+hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
+                              bool shared, int64_t T, int max_tiles, TileListKind kind,
+                              int32_t* tiles, hipStream_t s);
+hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
+                                const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s);
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
-                             const int32_t* counts, const int32_t* offsets, int32_t* tiles,
-                             int max_tiles, int64_t T, void* out, hipStream_t s);
+                             const int32_t* tiles, int max_tiles, int64_t T, void* out,
+                             hipStream_t s);
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                                     const int32_t* counts, const int32_t* offsets,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,

@@ -129,10 +129,67 @@ __device__ __forceinline__ int block_scan_1024(int v, int& excl, int* wsum) {
   return total;
 }
 
+// Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
+// fastest; the W wide items come first, then the N narrow ones. XCD x owns the x-th contiguous
+// eighth of the wide items and of the narrow items, so items that share a token tile run on
+// one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
+// (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
+// (short, HBM-bound) items, so that the launch ends on short items, and its other narrow items
+// are spread evenly between the wide (MFMA-bound) ones, so that weight streaming for small
+// experts overlaps MFMA work. Returns the item of workgroup b, or -1.
+constexpr int kTailSlots = 32;
+__device__ __forceinline__ int dispatch_item(int b, int W, int N) {
+  const int x = b & 7, j = b >> 3;
+  const int cw = (W + 7) >> 3, cn = (N + 7) >> 3;
+  const int w0 = min(W, x * cw), nw = min(W, w0 + cw) - w0;     // this XCD's wide items
+  const int n0 = min(N, x * cn), nn = min(N, n0 + cn) - n0;     // and narrow items
+  if (j >= nw + nn) return -1;
+  const int tail = min(nn, kTailSlots);
+  const int spread = nn - tail, prefix = nw + spread;
+  if (j >= prefix) return W + n0 + spread + (j - prefix);       // the tail: narrow items
+  // narrow items before slot j in the prefix: floor(j * spread / prefix)
+  const int before = static_cast<int>(static_cast<int64_t>(j) * spread / prefix);
+  const int upto = static_cast<int>(static_cast<int64_t>(j + 1) * spread / prefix);
+  return upto > before ? W + n0 + before : w0 + (j - before);
+}
+
+// Words of the tile list before the dispatch tables (entries, counts), rounded to 16 bytes.
+__host__ __device__ constexpr int64_t table_base(int max_tiles) {
+  return (2 * static_cast<int64_t>(max_tiles) + kTileListTail + 3) / 4 * 4;
+}
+
+// One entry of a dispatch table: the work of workgroup b of a bf16 GEMM launch, read with a
+// single 16-byte load: {group | weight tile << 16 (-1: none), first row | narrow flag,
+// group's first row in the sorted rows, group's row count}.
+__device__ __forceinline__ void write_dispatch(const int32_t* tiles, int max_tiles, int n_wtiles,
+                                              int wt_cols, int grid, const int32_t* counts,
+                                              const int32_t* offsets, int E, int T, int sh_row0,
+                                              int I, int Is, u32x4* table) {
+  const int n_all = tiles[2 * max_tiles], n_wide = tiles[2 * max_tiles + 1];
+  const int W = n_wide * n_wtiles, N = (n_all - n_wide) * n_wtiles;
+  for (int b = threadIdx.x; b < grid; b += blockDim.x) {
+    const int item = dispatch_item(b, W, N);
+    u32x4 ent = {0xffffffffu, 0u, 0u, 0u};
+    if (item >= 0) {
+      const int ti = item / n_wtiles, wt = item - ti * n_wtiles;
+      const int g = tiles[2 * ti];
+      const bool shared = g == E;
+      // weight tiles past a narrower shared expert (gate_up: wt_cols = kWM/2 channels) idle
+      if (wt_cols == 0 || wt * wt_cols < (shared ? Is : I))
+        ent = u32x4{static_cast<uint32_t>(g | (wt << 16)), static_cast<uint32_t>(tiles[2 * ti + 1]),
+                    static_cast<uint32_t>(shared ? sh_row0 : offsets[g]),
+                    static_cast<uint32_t>(shared ? T : counts[g])};
+    }
+    table[b] = ent;
+  }
+}
+
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
-                                                           int E, int shared, int T, int max_tiles,
-                                                           int wide, int narrow,
-                                                           int32_t* __restrict__ tiles) {
+                                                           const int32_t* __restrict__ offsets,
+                                                           int E, int shared, int T, int sh_row0,
+                                                           int max_tiles, int wide, int narrow,
+                                                           int I, int Is, int H, int grid_gu,
+                                                           int grid_dn, int32_t* __restrict__ tiles) {
   __shared__ int wsum[16];
   const int G = E + shared;
   const int tid = threadIdx.x;
@@ -167,6 +224,13 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     tiles[2 * max_tiles] = min(tw + tn, max_tiles);
     tiles[2 * max_tiles + 1] = min(tw, max_tiles);
   }
+  if (grid_gu + grid_dn == 0) return;
+  __syncthreads();                           // the list is complete (and visible to the block)
+  u32x4* tab = reinterpret_cast<u32x4*>(tiles + table_base(max_tiles));
+  write_dispatch(tiles, max_tiles, I > Is ? I / (kWM / 2) : Is / (kWM / 2), kWM / 2, grid_gu,
+                 counts, offsets, E, T, sh_row0, I, Is, tab);
+  write_dispatch(tiles, max_tiles, H / kWM, 0, grid_dn, counts, offsets, E, T, sh_row0, I, Is,
+                 tab + grid_gu);
 }
 
 // ---- one token tile --------------------------------------------------------------------------
@@ -432,47 +496,17 @@ void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
                                 gw.E, lds);
 }
 
-// Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
-// fastest; the W wide items come first, then the N narrow ones. XCD x owns the x-th contiguous
-// eighth of the wide items and of the narrow items, so items that share a token tile run on
-// one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
-// (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
-// (short, HBM-bound) items, so that the launch ends on short items, and its other narrow items
-// are spread evenly between the wide (MFMA-bound) ones, so that weight streaming for small
-// experts overlaps MFMA work. Returns the item of workgroup b, or -1.
-constexpr int kTailSlots = 32;
-__device__ __forceinline__ int dispatch_item(int b, int W, int N) {
-  const int x = b & 7, j = b >> 3;
-  const int cw = (W + 7) >> 3, cn = (N + 7) >> 3;
-  const int w0 = min(W, x * cw), nw = min(W, w0 + cw) - w0;     // this XCD's wide items
-  const int n0 = min(N, x * cn), nn = min(N, n0 + cn) - n0;     // and narrow items
-  if (j >= nw + nn) return -1;
-  const int tail = min(nn, kTailSlots);
-  const int spread = nn - tail, prefix = nw + spread;
-  if (j >= prefix) return W + n0 + spread + (j - prefix);       // the tail: narrow items
-  // narrow items before slot j in the prefix: floor(j * spread / prefix)
-  const int before = static_cast<int>(static_cast<int64_t>(j) * spread / prefix);
-  const int upto = static_cast<int>(static_cast<int64_t>(j + 1) * spread / prefix);
-  return upto > before ? W + n0 + before : w0 + (j - before);
-}
-
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
-                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ counts,
-                  const int32_t* __restrict__ perm_tok, const int32_t* __restrict__ tiles,
-                  int max_tiles, int n_wtiles, int T, uint16_t* __restrict__ dst, int dst_ld) {
+                  const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table, int T,
+                  uint16_t* __restrict__ dst, int dst_ld) {
   __shared__ u32x4 lds[kLdsU4];
-  const int n_all = tiles[2 * max_tiles], n_wide = tiles[2 * max_tiles + 1];
-  const int item = dispatch_item(blockIdx.x, n_wide * n_wtiles, (n_all - n_wide) * n_wtiles);
-  if (item < 0) return;
-  const int ti = item / n_wtiles, wt = item - ti * n_wtiles;
-  const int g = tiles[2 * ti], e = tiles[2 * ti + 1];
-  const bool shared = g == gw.E;
-  if (wt * (MODE == kGateUp ? kWM / 2 : kWM) >= (MODE == kGateUp ? (shared ? gw.Is : gw.I) : gw.H))
-    return;                                  // weight tile past a narrower shared expert
-  const int n = shared ? T : counts[g];
-  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  const u32x4 ent = table[blockIdx.x];
+  const int gx = static_cast<int>(ent[0]);
+  if (gx < 0) return;
+  const int g = gx & 0xffff, wt = gx >> 16, e = static_cast<int>(ent[1]);
+  const int row0 = static_cast<int>(ent[2]), n = static_cast<int>(ent[3]);
   if (e & kNarrowFlag)
     tile_product<MODE, Narrow>(gw, src, src_ld, perm_tok, g, e & (kNarrowFlag - 1), n, row0, wt,
                                dst, dst_ld, lds);
@@ -504,42 +538,55 @@ bool tiled_supported(const GroupWeights& gw) {
   constexpr int kBKmax = Wide::kBK > Narrow::kBK ? Wide::kBK : Narrow::kBK;
   return gw.H % kWM == 0 && gw.H % kBKmax == 0 && gw.I % (kWM / 2) == 0 &&
          (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBKmax == 0 &&
-         (gw.Is == 0 || gw.Is % kBKmax == 0) && gw.I < (1 << 20);
+         (gw.Is == 0 || gw.Is % kBKmax == 0) && gw.I < (1 << 20) && gw.E < (1 << 16) - 1;
 }
 
-hipError_t launch_build_tiles(const int32_t* counts, int E, bool shared, int64_t T, int max_tiles,
-                              TileListKind kind, int32_t* tiles, hipStream_t s) {
+// Workgroups of a bf16 GEMM launch: one per possible item; the per-XCD rounding of the two item
+// ranges adds at most 16 slots.
+static int item_grid(int max_tiles, int n_wtiles) {
+  return static_cast<int>(round8(static_cast<int64_t>(max_tiles) * n_wtiles + 16));
+}
+static int gate_up_wtiles(int I, int Is) { return (I > Is ? I : Is) / (kWM / 2); }
+static int down_wtiles(int H) { return H / kWM; }
+
+int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H) {
+  const int64_t slots = item_grid(max_tiles, gate_up_wtiles(I, Is)) +
+                        item_grid(max_tiles, down_wtiles(H));
+  return table_base(max_tiles) * 4 + slots * 16;
+}
+
+hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
+                              bool shared, int64_t T, int max_tiles, TileListKind kind,
+                              int32_t* tiles, hipStream_t s) {
   int wide, narrow;
   tile_widths(kind, wide, narrow);
-  build_tiles_kernel<<<1, 1024, 0, s>>>(counts, E, shared ? 1 : 0, static_cast<int>(T), max_tiles,
-                                        wide, narrow, tiles);
+  const bool tables = kind == kTilesBf16;
+  const int grid_gu = tables ? item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is)) : 0;
+  const int grid_dn = tables ? item_grid(max_tiles, down_wtiles(gw.H)) : 0;
+  build_tiles_kernel<<<1, 1024, 0, s>>>(counts, offsets, gw.E, shared ? 1 : 0,
+                                        static_cast<int>(T), gw.sh_row0, max_tiles, wide, narrow,
+                                        gw.I, gw.Is, gw.H, grid_gu, grid_dn, tiles);
   return hipGetLastError();
 }
 
-// One workgroup per item; per-XCD rounding of the two item ranges adds at most 16 slots.
-static unsigned item_grid(int max_tiles, int n_wtiles) {
-  return round8(static_cast<int64_t>(max_tiles) * n_wtiles + 16);
-}
-
-hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* counts,
-                                const int32_t* offsets, const int32_t* perm_tok,
-                                int32_t* tiles, int max_tiles, int64_t T, int act_ld,
+hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
+                                const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s) {
-  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const int n_wtiles = Imax / (kWM / 2);
-  tiled_kernel<kGateUp><<<item_grid(max_tiles, n_wtiles), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(x), gw.H, offsets, counts, perm_tok, tiles, max_tiles,
-      n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
+  const auto* table = reinterpret_cast<const u32x4*>(tiles + table_base(max_tiles));
+  tiled_kernel<kGateUp><<<item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is)), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), gw.H, perm_tok, table, static_cast<int>(T),
+      static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
 }
 
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
-                             const int32_t* counts, const int32_t* offsets, int32_t* tiles,
-                             int max_tiles, int64_t T, void* out, hipStream_t s) {
-  const int n_wtiles = gw.H / kWM;
-  tiled_kernel<kDown><<<item_grid(max_tiles, n_wtiles), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(act), act_ld, offsets, counts, nullptr, tiles, max_tiles,
-      n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
+                             const int32_t* tiles, int max_tiles, int64_t T, void* out,
+                             hipStream_t s) {
+  const auto* table = reinterpret_cast<const u32x4*>(tiles + table_base(max_tiles)) +
+                      item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is));
+  tiled_kernel<kDown><<<item_grid(max_tiles, down_wtiles(gw.H)), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(act), act_ld, nullptr, table, static_cast<int>(T),
+      static_cast<uint16_t*>(out), gw.H);
   return hipGetLastError();
 }
 
