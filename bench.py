@@ -247,6 +247,11 @@ def main():
             "hit_experts": p["hit_experts"], "max_tokens_per_expert": p["max_tokens_per_expert"],
             "stage_us": {k_: round(v, 1) for k_, v in p["stage_us"].items()},
             "gate_up_tflops": round(pgf / (pgu * 1e-6) / 1e12, 2),
+            "roofline": {"kernel": "tiled_kernel<kGateUp>", "bound": "mfma",
+                         "achieved": round(pgf / (pgu * 1e-6) / 1e12, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s",
+                         "frac": round(pgf / (pgu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_flops_per_launch": pgf, "avg_launch_us": round(pgu, 1)},
         }
         del pblk, px
 
@@ -276,6 +281,9 @@ def main():
         "layer_frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
         "hit_experts": d["hit_experts"],
         "stage_us": {k_: round(v, 2) for k_, v in d["stage_us"].items()},
+        "stage_note": ("stage_us: HIP events between the stages of lbmoe_forward_profiled calls "
+                       "(one call at a time); us_per_call: back-to-back lbmoe_forward calls, which "
+                       "run under the sustained power limit and so slower per stage"),
         "roofline": {"kernel": "gate_up_bf16_kernel", "bound": "hbm", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": gb,
