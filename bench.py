@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the other configurations (decode sweep, E=512 layer, fp8 variant)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="also run a plain copy kernel (torch.neg, fp32) over this many MiB, "
                         "3 times: the calibration dispatch for FETCH_SIZE/WRITE_SIZE counters")
@@ -144,12 +146,15 @@ def measure(blk, x, steps, warmup, hip):
             "max_tokens_per_expert": int(counts.max()), "y": y}
 
 
-def work(shape, T, n_hit):
-    """Algorithmic bytes/flops of the layer and of its gate_up kernel."""
+def work(shape, T, n_hit, wb=2):
+    """Algorithmic bytes/flops of the layer and of its gate_up kernel (wb: bytes per expert
+    weight element; fp8 adds its per-128x128-block fp32 scales)."""
     H, E, k, I, Is = (shape.hidden_size, shape.num_experts, shape.top_k,
                       shape.moe_intermediate_size, shape.shared_expert_intermediate_size)
-    wb = 2
-    layer_bytes = n_hit * 3 * H * I * wb + (3 * H * Is * wb + H * 2 if Is else 0) + E * H * 2 + 2 * T * H * 2
+    sc = 3 * (H // 128) * (I // 128) * 4 if wb == 1 else 0      # scale bytes per expert
+    scs = 3 * (H // 128) * (Is // 128) * 4 if wb == 1 and Is else 0
+    layer_bytes = (n_hit * (3 * H * I * wb + sc) + (3 * H * Is * wb + scs + H * 2 if Is else 0)
+                   + E * H * 2 + 2 * T * H * 2)
     layer_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * E * H
     gu_bytes = n_hit * 2 * I * H * wb + (2 * Is * H * wb if Is else 0) + T * H * 2 + (T * k * I + (T * Is if Is else 0)) * 2
     gu_flops = 2 * T * k * 2 * H * I + 2 * T * 2 * H * Is
@@ -200,6 +205,85 @@ def cpu_baseline(blk, x, zipf, budget_s):
     times.sort()
     return {"us_per_call": times[len(times) // 2] * 1e6, "cores": ncores, "calls": len(times),
             "algorithm": algorithm}
+
+
+def measure_wall(blks, x, steps, warmup):
+    """Back-to-back lbmoe_forward calls cycling over `blks` (copies of one layer, so that the
+    weights touched per call exceed the 256 MB MALL); returns (us per call, experts hit)."""
+    import torch
+    from layerbatch_amd import _lib
+    T = x.shape[0]
+    lib = _lib.lib()
+    stream = _lib.stream_of(x.device)
+    y = torch.empty_like(x)
+    calls = []
+    for blk in blks:
+        L = blk.layer()
+        ws = torch.empty(_lib.workspace_size(L, T), dtype=torch.uint8, device=x.device)
+        calls.append((L, ws, (ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws),
+                              ws.numel(), stream)))
+    for i in range(warmup):
+        _lib.check(lib.lbmoe_forward(*calls[i % len(calls)][2]), "lbmoe_forward")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        lib.lbmoe_forward(*calls[i % len(calls)][2])
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    L, ws, _ = calls[0]
+    off, _ = _lib.workspace_region(L, T, "counts")
+    counts = ws[off:off + 4 * L.num_experts].view(torch.int32).cpu()
+    return us, int((counts > 0).sum())
+
+
+def extra_configs(dev, steps):
+    """The other configurations of the measurement plan, each at one GPU: the decode sweep of
+    the headline layer, the Qwen3-Next-style E=512 layer with a shared expert, and its fp8
+    variant. Every entry: back-to-back us per call and the algorithmic rate."""
+    import torch
+    from layerbatch_amd.synth import SHAPES, make_x
+    out = []
+
+    def entry(name, shape, T, us, hit, wb, bound):
+        lb, lf, _, _ = work(shape, T, hit, wb)
+        gbs = lb / (us * 1e-6) / 1e9
+        tf = lf / (us * 1e-6) / 1e12
+        peak_tf = FP8_PEAK_TFLOPS if wb == 1 else BF16_PEAK_TFLOPS
+        return {"config": name, "T": T, "us_per_call": round(us, 1), "hit_experts": hit,
+                "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "TFLOPs": round(tf, 2), "frac_of_mfma_peak": round(tf / peak_tf, 4),
+                "bound": bound}
+
+    # decode sweep of the headline layer; four weight copies rotate when a call touches few
+    # experts, so the weights do not stay in the 256 MB MALL between calls
+    shape = SHAPES["qwen3-30b-a3b"]
+    blk, _ = layer_inputs(shape, 1, 0, False, dev)
+    copies = [blk] + [layer_inputs(shape, 1, 1 + i, False, dev)[0] for i in range(3)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    for T in (1, 16, 64, 256):
+        x = make_x(g, T, shape.hidden_size, device=dev)
+        blks = copies if T <= 16 else copies[:1]
+        us, hit = measure_wall(blks, x, steps, max(2, steps // 5))
+        out.append(entry("qwen3-30b-a3b decode" + (" (4 weight copies rotating)" if T <= 16 else ""),
+                         shape, T, us, hit, 2, "hbm"))
+    del blk, copies
+    torch.cuda.empty_cache()
+
+    shape = SHAPES["qwen3-next-e512"]
+    for fp8 in (False, True):
+        blk, _ = layer_inputs(shape, 1, 0, False, dev, fp8=fp8)
+        for T in ((128, 16384) if fp8 else (128, 4096)):
+            x = make_x(g, T, shape.hidden_size, device=dev)
+            n = steps if T <= 256 else max(3, steps // 5)
+            us, hit = measure_wall([blk], x, n, max(1, n // 5))
+            out.append(entry("qwen3-next-e512" + (" fp8-e4m3" if fp8 else "") +
+                             (" prefill" if T > 256 else " decode"), shape, T, us, hit,
+                             1 if fp8 else 2, "mfma" if fp8 and T > 256 else "hbm"))
+            del x
+        del blk
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -255,6 +339,8 @@ def main():
         }
         del pblk, px
 
+    extra = None if args.no_extra else extra_configs(dev, args.steps)
+
     if args.copy_probe_mib:
         n = args.copy_probe_mib << 18
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -290,6 +376,7 @@ def main():
                      "avg_launch_us": round(gu_us, 2)},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "extra": extra,
     }
     print(json.dumps(out))
 
