@@ -1,18 +1,19 @@
 // LDS-tiled grouped GEMMs for prefill-sized batches (gfx950, v_mfma_f32_32x32x16_bf16).
 //
 // Same products as the streaming kernels (gate_up + SiLU*mul, qwen3_5.py:835-836; down,
-// qwen3_5.py:837), for groups with many tokens: a workgroup of 4 waves (2 x 2) multiplies a
-// tile of kWM = 256 weight rows by a tile of tokens of one expert, staging both operands
+// qwen3_5.py:837), for groups with many tokens: a workgroup of 8 waves (two per SIMD, so one
+// wave's copy issue and LDS waits overlap the other's MFMAs) multiplies a tile of kWM = 256
+// weight rows by a tile of tokens of one expert, staging both operands
 // through LDS in k-tiles, so each operand byte fetched from L2 feeds many MFMA columns. The
 // k-tiles move global -> LDS directly (global_load_lds_dwordx4, no register staging) through
 // a ring of LDS buffers that is filled kStages k-tiles ahead of the MFMAs.
 //
-// Two token-tile widths share one launch. A wide tile (256 tokens, each wave 128 x 128) moves
+// Two token-tile widths share one launch. A wide tile (256 tokens, each wave 128 x 64) moves
 // the fewest operand bytes per flop, which matters here: with the whole chip busy the shader
 // clock settles near 1.5 GHz and every byte moved between L2 and LDS costs cycles and power.
-// A narrow tile (64 tokens, each wave 128 x 32) serves the few tokens that small experts get
+// A narrow tile (128 tokens, each wave 128 x 32) serves the few tokens that small experts get
 // under a skewed router: such a tile is bound by streaming the expert's weights from HBM, and
-// a wide tile would spend 4x the MFMA work on padding. Because the tile list follows expert
+// a wide tile would spend twice the MFMA work on padding. Because the tile list follows expert
 // order, narrow (HBM-bound) and wide (MFMA-bound) tiles run side by side.
 //
 // Work list. build_tiles turns the per-expert token counts into a list of (group, first row |
@@ -26,20 +27,17 @@
 // four consecutive output channels of one token are stored together. LDS rows are kBK bf16 in
 // 16-byte chunks; chunk j of row r is stored at a row-dependent XOR of j (swz), which keeps
 // the 32-row MFMA operand reads free of bank conflicts.
-// Gate_up workgroups take kWM/2 channels: wave row-half h holds gate rows then up rows of the
-// same kWM/4 channels, so SiLU*mul pairs accumulators in registers.
+// Gate_up workgroups take kWM/2 channels: the weight rows of wave row-block h are the gate rows
+// then the up rows of the same channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
 #include "internal.hpp"
 #include "tiled_common.hpp"
 
 namespace lbmoe {
 
-constexpr int kWavesM = 2;                          // waves along the weight rows
-constexpr int kWavesN = 2;                          // waves along the tokens
-constexpr int kWaves = kWavesM * kWavesN;
+constexpr int kWaves = 8;                           // two waves per SIMD
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMT = 4;                              // 32-row MFMA tiles per wave (weights)
-constexpr int kWM = kWavesM * kMT * 32;             // weight rows per workgroup
+constexpr int kWM = 256;                            // weight rows per workgroup
 
 #ifndef LBMOE_TILE_BK
 #define LBMOE_TILE_BK 64
@@ -54,10 +52,15 @@ constexpr int kWM = kWavesM * kMT * 32;             // weight rows per workgroup
 #define LBMOE_NARROW_STAGES 3
 #endif
 
-// One token-tile shape: NT 32-column MFMA tiles per wave, k-tiles of BK, STAGES LDS buffers.
-template <int NT, int BK, int STAGES>
+// One token-tile shape: WAVES_M x (kWaves / WAVES_M) waves, each owning MT x NT 32x32 MFMA
+// tiles (weights x tokens), k-tiles of BK, STAGES LDS buffers.
+template <int WAVES_M, int MT, int NT, int BK, int STAGES>
 struct TileShape {
+  static constexpr int kWavesM = WAVES_M;
+  static constexpr int kWavesN = kWaves / WAVES_M;
+  static constexpr int kMT = MT;
   static constexpr int kNT = NT;
+  static constexpr int kRW = MT * 32;                         // weight rows per wave
   static constexpr int kWT = kWavesN * NT * 32;               // tokens per workgroup
   static constexpr int kBK = BK;
   static constexpr int kStages = STAGES;
@@ -71,19 +74,25 @@ struct TileShape {
   // Chunk j of row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
   // kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
   static constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
+  static_assert(WAVES_M * MT * 32 == kWM, "waves must tile the weight rows");
   static_assert(kChunks == 4 || kChunks == 8, "BK must be 32 or 64");
   static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
                 "copies must tile the stage");
   static_assert(kKSteps % 2 == 0, "the next k-tile's first fragments go to register buffer 0");
+  static_assert(MT % 2 == 0, "gate_up pairs a wave's gate tiles with its up tiles");
   static __device__ __forceinline__ int swz(int r, int j) {
     return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
   }
 };
-using Wide = TileShape<4, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
-using Narrow = TileShape<1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
+// wide: 2 x 4 waves of 128 x 64 (256 tokens); narrow: 2 x 4 waves of 128 x 32 (128 tokens)
+using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
+using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
+// router logits: 4 x 2 waves of 64 x 32 (64 tokens), so that T = 8192 gives 128 workgroups
+using RouterShape = TileShape<4, 2, 1, 64, 3>;
 constexpr int kLdsU4 = Wide::kStages * Wide::kStageU4 > Narrow::kStages * Narrow::kStageU4
                            ? Wide::kStages * Wide::kStageU4
                            : Narrow::kStages * Narrow::kStageU4;
+static_assert(RouterShape::kStages * RouterShape::kStageU4 <= kLdsU4, "router ring too large");
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
 
 constexpr int32_t kNarrowFlag = 1 << 30;
@@ -248,7 +257,8 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
                                              uint16_t* __restrict__ dst, int dst_ld,
                                              u32x4* __restrict__ lds) {
   constexpr bool GATEUP = MODE == kGateUp, ROUTER = MODE == kRouter;
-  constexpr int kNT = S::kNT, kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
+  constexpr int kMT = S::kMT, kNT = S::kNT, kRW = S::kRW, kWavesM = S::kWavesM;
+  constexpr int kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
   constexpr int kRowsPerLoad = S::kRowsPerLoad, kALoads = S::kALoads, kBLoads = S::kBLoads;
   constexpr int kLoads = S::kLoads, kKSteps = S::kKSteps, kStageU4 = S::kStageU4;
   constexpr int kSwzShift = S::kSwzShift;
@@ -291,9 +301,10 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     int grow;
     const uint16_t* base = wbase;
     if (GATEUP) {
-      const int half = row / (kWM / 2), sub = row % (kWM / 2);
-      base = sub < kWM / 4 ? wbase : wup;
-      grow = c0 + half * (kWM / 4) + (sub % (kWM / 4));
+      // wave h's rows: the gate rows then the up rows of channels c0 + h*kRW/2 .. +kRW/2
+      const int half = row / kRW, sub = row % kRW;
+      base = sub < kRW / 2 ? wbase : wup;
+      grow = c0 + half * (kRW / 2) + (sub % (kRW / 2));
     } else if (ROUTER) {
       grow = min(c0 + row, gw.E - 1);      // rows past E repeat a valid row; not stored
     } else {
@@ -349,7 +360,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   auto read_frags = [&](const u32x4* cur, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
     const int j = 2 * ks + mk;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) fa[i] = cur[S::swz(wm * (kWM / 2) + 32 * i + mr, j)];
+    for (int i = 0; i < kMT; ++i) fa[i] = cur[S::swz(wm * kRW + 32 * i + mr, j)];
 #pragma unroll
     for (int t = 0; t < kNT; ++t) fb[t] = cur[S::swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
   };
@@ -443,7 +454,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
           for (int v = 0; v < 4; ++v)
             a[v] = GATEUP ? silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v]
                           : acc[i][t][4 * v4 + v];
-          const int c = (GATEUP ? wm * (kWM / 4) : wm * (kWM / 2)) + 32 * i + 8 * v4 + rq;
+          const int c = (GATEUP ? wm * (kRW / 2) : wm * kRW) + 32 * i + 8 * v4 + rq;
           *reinterpret_cast<u32x2*>(st + slot(r, c / 8) * 16 + (c % 8) * 2) =
               u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
@@ -468,7 +479,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       for (int i = 0; i < kMT; ++i)
 #pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) {
-          const int e = c0 + wm * (kWM / 2) + 32 * i + 8 * v4 + rq;
+          const int e = c0 + wm * kRW + 32 * i + 8 * v4 + rq;
           if (e + 3 < E && (E & 3) == 0) {
             *reinterpret_cast<u32x2*>(orow + e) =
                 u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
@@ -484,20 +495,20 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 }
 
 // ---- the kernels -----------------------------------------------------------------------------
-// Router logits: one workgroup per (token tile of Narrow::kWT, weight tile), no tile list.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// Router logits: one workgroup per (token tile of RouterShape::kWT, weight tile), no tile list.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T, int n_wtiles,
                          uint16_t* __restrict__ logits) {
   __shared__ u32x4 lds[kLdsU4];
-  const int logical = xcd_item(blockIdx.x, (T + Narrow::kWT - 1) / Narrow::kWT * n_wtiles);
+  const int logical = xcd_item(blockIdx.x, (T + RouterShape::kWT - 1) / RouterShape::kWT * n_wtiles);
   if (logical < 0) return;
   const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  tile_product<kRouter, Narrow>(gw, x, gw.H, nullptr, 0, ti * Narrow::kWT, T, 0, wt, logits,
-                                gw.E, lds);
+  tile_product<kRouter, RouterShape>(gw, x, gw.H, nullptr, 0, ti * RouterShape::kWT, T, 0, wt,
+                                     logits, gw.E, lds);
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
                   const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table, int T,
                   uint16_t* __restrict__ dst, int dst_ld) {
@@ -590,7 +601,7 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
   return hipGetLastError();
 }
 
-bool tiled_router_supported(int E, int H) { return H % Narrow::kBK == 0 && E >= 1; }
+bool tiled_router_supported(int E, int H) { return H % RouterShape::kBK == 0 && E >= 1; }
 
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s) {
@@ -599,7 +610,7 @@ hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, 
   gw.E = E;
   gw.H = H;
   const int n_wtiles = (E + kWM - 1) / kWM;
-  const int64_t n_ttiles = (T + Narrow::kWT - 1) / Narrow::kWT;
+  const int64_t n_ttiles = (T + RouterShape::kWT - 1) / RouterShape::kWT;
   router_tiled_kernel<<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), static_cast<int>(T), n_wtiles,
       static_cast<uint16_t*>(logits));
