@@ -1,0 +1,112 @@
+"""GPU parity at the measured workloads' full sizes.
+
+Every routing decision is checked exactly: router logits on sampled rows against the exact dot
+products, selection on all rows against the oracle's selection from the GPU's own logits, and
+the whole permutation. The layer output is checked against the float64 oracle on sampled rows;
+the oracle only ever touches the experts those rows selected, which are copied off the GPU one
+at a time.
+"""
+import numpy as np
+import pytest
+import torch
+
+from layerbatch_amd.synth import SHAPES, make_layer, make_x, zipf_bias
+from oracle import moe as om
+from tests import gpu_checks as gc
+from tests.helpers import bf16_bits_of, to_np
+from tests.test_gpu_parity import _block, _region
+
+pytestmark = pytest.mark.gpu
+
+
+class _Experts:
+    """Per-expert view of a device tensor [E, ...] for the oracle: expert e is copied to the
+    host when first indexed (bf16 as float32, other dtypes as they are; the last one is kept)."""
+
+    def __init__(self, t):
+        self.t = t
+        self.shape = tuple(t.shape)
+        self._e, self._a = None, None
+
+    def __getitem__(self, e):
+        e = int(e)
+        if e != self._e:
+            a = self.t[e]
+            self._e, self._a = e, (a.float() if a.dtype == torch.bfloat16 else a).cpu().numpy()
+        return self._a
+
+
+def _run_full(shape, T, device, seed, zipf, sample, fp8=False):
+    w, g = make_layer(shape, seed=seed, device=device)
+    x = make_x(g, T, shape.hidden_size, device=device)
+    blk = _block(shape, w, device)
+    if zipf:
+        blk.gate.logit_bias = zipf_bias(g, shape.num_experts, device=device)
+    if fp8:
+        blk.quantize_fp8_()
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=device)
+    y = blk(x, workspace=ws)
+    torch.cuda.synchronize()
+    E, k = shape.num_experts, shape.top_k
+    rows = np.unique(np.random.default_rng(seed).choice(T, size=min(sample, T), replace=False))
+    xn = to_np(x)
+    logits = to_np(_region(blk, ws, T, "logits", torch.bfloat16, (T, E)))
+    wg = to_np(w["gate"])
+    gc.check_logits(bf16_bits_of(_region(blk, ws, T, "logits", torch.bfloat16, (T, E)))[rows],
+                    xn[rows], wg)
+    bias = None if blk.gate.logit_bias is None else blk.gate.logit_bias.cpu().numpy()
+    topw = _region(blk, ws, T, "topk_w", torch.bfloat16, (T, k))
+    idx = to_np(_region(blk, ws, T, "topk_idx", torch.int32, (T, k)))
+    _, idx_ref = gc.check_route(idx, bf16_bits_of(topw), logits, bias, k)
+    V = T * k
+    gc.check_permutation(idx_ref, E,
+                         to_np(_region(blk, ws, T, "counts", torch.int32, (E,))),
+                         to_np(_region(blk, ws, T, "offsets", torch.int32, (E + 1,))),
+                         to_np(_region(blk, ws, T, "perm_tok", torch.int32, (V,))),
+                         to_np(_region(blk, ws, T, "perm_slot", torch.int32, (V,))),
+                         to_np(_region(blk, ws, T, "inv", torch.int32, (T, k))))
+    tw = to_np(topw)[rows]
+    shared = shape.shared_expert_intermediate_size > 0
+    if fp8:
+        ex = blk.experts
+        y_ref = om.experts_fp8(xn[rows], idx_ref[rows], tw, _Experts(ex.gate_up_q),
+                               _Experts(ex.gate_up_scale), _Experts(ex.down_q),
+                               _Experts(ex.down_scale))
+        if shared:
+            se = blk.shared_expert
+            q = [a.cpu().numpy() for n in ("gate", "up", "down") for a in se.q[n]]
+            gsh = om.shared_gate(xn[rows], to_np(w["sh_gate_w"])).astype(np.float64)
+            y_ref = y_ref + gsh[:, None] * om.shared_expert_fp8(xn[rows], *q)
+        tol = gc.TOL_FP8
+    else:
+        y_ref = om.experts(xn[rows], idx_ref[rows], tw, _Experts(w["gate_up"]), _Experts(w["down"]))
+        if shared:
+            gsh = om.shared_gate(xn[rows], to_np(w["sh_gate_w"])).astype(np.float64)
+            y_ref = y_ref + gsh[:, None] * om.shared_expert(
+                xn[rows], to_np(w["sh_gate"]), to_np(w["sh_up"]), to_np(w["sh_down"]))
+        tol = gc.TOL_BF16
+    return gc.check_output(to_np(y)[rows], y_ref, tol)
+
+
+@pytest.mark.parametrize("T", [128, 256])
+def test_fullsize_decode_qwen3_30b(gpu, T):
+    """Qwen3-30B-A3B layer (H=2048, E=128, top-8, I=768), decode batches."""
+    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=1, zipf=False, sample=24)
+
+
+def test_fullsize_prefill_qwen3_30b_zipf(gpu):
+    """The same layer at T=8192 with the Zipf(1.2) router bias: empty experts, a hot expert
+    with thousands of tokens, wide and narrow tiles."""
+    _run_full(SHAPES["qwen3-30b-a3b"], 8192, gpu, seed=0, zipf=True, sample=24)
+
+
+@pytest.mark.parametrize("T", [128, 4096])
+def test_fullsize_e512_shared(gpu, T):
+    """Qwen3-Next-style layer: H=2048, E=512, top-10, I=512, shared expert Is=512."""
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=2, zipf=False, sample=16)
+
+
+@pytest.mark.parametrize("T", [128, 16384])
+def test_fullsize_e512_fp8(gpu, T):
+    """The E=512 layer with e4m3 weights and activations (per-block fp32 scales)."""
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=3, zipf=False, sample=8, fp8=True)
