@@ -169,29 +169,32 @@ __host__ __device__ constexpr int64_t table_base(int max_tiles) {
 
 // One entry of a dispatch table: the work of workgroup b of a bf16 GEMM launch, read with a
 // single 16-byte load: {group | weight tile << 16 (-1: none), first row | narrow flag,
-// group's first row in the sorted rows, group's row count}.
-__device__ __forceinline__ void write_dispatch(const int32_t* tiles, int max_tiles, int n_wtiles,
-                                              int wt_cols, int grid, const int32_t* counts,
-                                              const int32_t* offsets, int E, int T, int sh_row0,
-                                              int I, int Is, u32x4* table) {
-  const int n_all = tiles[2 * max_tiles], n_wide = tiles[2 * max_tiles + 1];
+// group's first row in the sorted rows, group's row count}. list: the tile list (2 ints per
+// entry); grp: per group (first row, row count).
+__device__ __forceinline__ void write_dispatch(const int* list, const int2* grp, int n_all,
+                                              int n_wide, int n_wtiles, int wt_cols, int grid,
+                                              int E, int I, int Is, u32x4* table) {
   const int W = n_wide * n_wtiles, N = (n_all - n_wide) * n_wtiles;
   for (int b = threadIdx.x; b < grid; b += blockDim.x) {
     const int item = dispatch_item(b, W, N);
     u32x4 ent = {0xffffffffu, 0u, 0u, 0u};
     if (item >= 0) {
       const int ti = item / n_wtiles, wt = item - ti * n_wtiles;
-      const int g = tiles[2 * ti];
-      const bool shared = g == E;
+      const int g = list[2 * ti];
       // weight tiles past a narrower shared expert (gate_up: wt_cols = kWM/2 channels) idle
-      if (wt_cols == 0 || wt * wt_cols < (shared ? Is : I))
-        ent = u32x4{static_cast<uint32_t>(g | (wt << 16)), static_cast<uint32_t>(tiles[2 * ti + 1]),
-                    static_cast<uint32_t>(shared ? sh_row0 : offsets[g]),
-                    static_cast<uint32_t>(shared ? T : counts[g])};
+      if (wt_cols == 0 || wt * wt_cols < (g == E ? Is : I)) {
+        const int2 gr = grp[g];
+        ent = u32x4{static_cast<uint32_t>(g | (wt << 16)), static_cast<uint32_t>(list[2 * ti + 1]),
+                    static_cast<uint32_t>(gr.x), static_cast<uint32_t>(gr.y)};
+      }
     }
     table[b] = ent;
   }
 }
+
+// Tile lists up to this many entries are also assembled in LDS, where the dispatch tables
+// read them back; longer ones are read back from memory.
+constexpr int kLdsListEntries = 4096;
 
 __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
                                                            const int32_t* __restrict__ offsets,
@@ -200,13 +203,18 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
                                                            int I, int Is, int H, int grid_gu,
                                                            int grid_dn, int32_t* __restrict__ tiles) {
   __shared__ int wsum[16];
+  __shared__ int s_list[2 * kLdsListEntries];
+  __shared__ int2 s_grp[1025];
   const int G = E + shared;
   const int tid = threadIdx.x;
+  const bool in_lds = max_tiles <= kLdsListEntries;
   const int per = (G + 1023) / 1024;
   const int lo = min(G, tid * per), hi = min(G, lo + per);
   int lw = 0, ln = 0, nw, nn;
   for (int g = lo; g < hi; ++g) {
-    group_tiles(g < E ? counts[g] : T, wide, narrow, nw, nn);
+    const int n = g < E ? counts[g] : T;
+    s_grp[g] = int2{g < E ? offsets[g] : sh_row0, n};
+    group_tiles(n, wide, narrow, nw, nn);
     lw += nw;
     ln += nn;
   }
@@ -214,32 +222,32 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   const int tw = block_scan_1024(lw, pw, wsum);
   const int tn = block_scan_1024(ln, pn, wsum);
   pn += tw;
+  auto put = [&](int pos, int g, int e) {
+    if (pos >= max_tiles) return;
+    tiles[2 * pos] = g;
+    tiles[2 * pos + 1] = e;
+    if (in_lds) {
+      s_list[2 * pos] = g;
+      s_list[2 * pos + 1] = e;
+    }
+  };
   for (int g = lo; g < hi; ++g) {
-    group_tiles(g < E ? counts[g] : T, wide, narrow, nw, nn);
-    for (int i = 0; i < nw; ++i, ++pw) {
-      if (pw < max_tiles) {
-        tiles[2 * pw] = g;
-        tiles[2 * pw + 1] = i * wide;
-      }
-    }
-    for (int i = 0; i < nn; ++i, ++pn) {
-      if (pn < max_tiles) {
-        tiles[2 * pn] = g;
-        tiles[2 * pn + 1] = (nw * wide + i * narrow) | kNarrowFlag;
-      }
-    }
+    group_tiles(s_grp[g].y, wide, narrow, nw, nn);
+    for (int i = 0; i < nw; ++i) put(pw++, g, i * wide);
+    for (int i = 0; i < nn; ++i) put(pn++, g, (nw * wide + i * narrow) | kNarrowFlag);
   }
+  const int n_all = min(tw + tn, max_tiles), n_wide = min(tw, max_tiles);
   if (tid == 0) {
-    tiles[2 * max_tiles] = min(tw + tn, max_tiles);
-    tiles[2 * max_tiles + 1] = min(tw, max_tiles);
+    tiles[2 * max_tiles] = n_all;
+    tiles[2 * max_tiles + 1] = n_wide;
   }
   if (grid_gu + grid_dn == 0) return;
   __syncthreads();                           // the list is complete (and visible to the block)
+  const int* list = in_lds ? s_list : tiles;
   u32x4* tab = reinterpret_cast<u32x4*>(tiles + table_base(max_tiles));
-  write_dispatch(tiles, max_tiles, I > Is ? I / (kWM / 2) : Is / (kWM / 2), kWM / 2, grid_gu,
-                 counts, offsets, E, T, sh_row0, I, Is, tab);
-  write_dispatch(tiles, max_tiles, H / kWM, 0, grid_dn, counts, offsets, E, T, sh_row0, I, Is,
-                 tab + grid_gu);
+  write_dispatch(list, s_grp, n_all, n_wide, I > Is ? I / (kWM / 2) : Is / (kWM / 2), kWM / 2,
+                 grid_gu, E, I, Is, tab);
+  write_dispatch(list, s_grp, n_all, n_wide, H / kWM, 0, grid_dn, E, I, Is, tab + grid_gu);
 }
 
 // ---- one token tile --------------------------------------------------------------------------
