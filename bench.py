@@ -2,17 +2,20 @@
 """Benchmark of the MoE feed-forward layer on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--T 128] [--prefill-T 8192] [--no-cpu-baseline]
+                    [--no-prefill] [--no-extra] [--copy-probe-mib N]
 
 Headline workload: the Qwen3-30B-A3B MoE layer (H=2048, E=128, top-8, I=768, bf16 weights
 ~N(0,0.02), activations ~N(0,1), synthetic, seed 0) at decode T=128. One step is one call of
 the whole layer (router -> permute -> gate_up+SiLU*mul -> down -> combine) on inputs already
 resident in HBM. The same run also measures the prefill chunk T=8192 with a Zipf(1.2)
-router bias (skewed expert loads).
+router bias (skewed expert loads), and (under "extra") the decode sweep T=1..256, the
+Qwen3-Next-style E=512 layer with a shared expert and its fp8-e4m3 variant.
 
 Printed: one JSON line. `value` is the layer's algorithmic HBM throughput in GB/s at T=128
-(hit experts' weights + router weight + x in + y out, divided by the wall time per call).
-`roofline` describes the dominant kernel (gate_up), timed with HIP events recorded on the
-library's stream around that kernel in every timed call. `cpu_baseline` times the torch-CPU
+(hit experts' weights + router weight + x in + y out, divided by the wall time of back-to-back
+calls). `roofline` describes the dominant kernel (gate_up), timed with HIP events recorded on
+the library's stream around that kernel in profiled calls; its `traffic` comes from the
+committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary. `cpu_baseline` times the torch-CPU
 restatement of the reference's decode algorithm (dense gather + bmm) on the host's cores.
 """
 import argparse

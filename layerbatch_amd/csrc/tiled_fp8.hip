@@ -1,6 +1,8 @@
 // LDS-tiled grouped GEMMs with fp8 (OCP e4m3) weights and activations, for prefill-sized
-// batches. Same work list, XCD order and global->LDS ring as the bf16 tiled kernels
-// (tiled_gemm.hip); the products are those of the fp8 streaming kernels (fp8.hip).
+// batches. They take a tile list of kFp8TileTokens-token tiles from build_tiles
+// (tiled_gemm.hip), deal its (token tile, weight tile) items to the XCDs in contiguous chunks
+// (xcd_item), and stage operands through a global->LDS ring; the products are those of the
+// fp8 streaming kernels (fp8.hip).
 //
 // A k-stage is 128 k = 128 bytes per row = exactly one 128-k scale block, and one
 // v_mfma_scale_f32_16x16x128_f8f6f4 covers a 16 x 16 tile over the whole block (lane
