@@ -35,11 +35,8 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
   w.bytes[R_HIST] = E * nblk * 4;
   w.bytes[R_BASE] = E * nblk * 4;
   w.bytes[R_LRANK] = V * 4;
-  w.bytes[R_TILES] =
-      std::max<int64_t>(tiled_list_bytes(tiled_max_tiles(Vs, E + 1, kTilesBf16), L.moe_intermediate_size,
-                                         L.shared_intermediate_size, H),
-                        (2 * static_cast<int64_t>(tiled_max_tiles(Vs, E + 1, kTilesFp8)) +
-                         kTileListTail) * 4);
+  w.bytes[R_TILES] = tiled_list_bytes(tiled_max_tiles(Vs, E + 1), L.moe_intermediate_size,
+                                      L.shared_intermediate_size, H);
   if (is_fp8(L)) {
     w.bytes[R_XQ] = T * H;
     w.bytes[R_XS] = T * (H / 128) * 4;
@@ -200,17 +197,14 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     float* acts = at<float>(ws, w, R_ACTS);
     const int64_t rows = T * k + (with_shared ? T : 0);
     LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
-    if (use_tiled(gw, T, k)) {
+    if (use_tiled(gw, T, k) && tiled_fp8_supported(gw)) {
       int32_t* tiles = at<int32_t>(ws, w, R_TILES);
-      const int max_tiles = tiled_max_tiles(rows, gw.groups, kTilesFp8);
-      LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, kTilesFp8,
-                                   tiles, s));
-      LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, counts, offsets, perm_tok, tiles, max_tiles,
-                                         T, Imax, act, s));
+      const int max_tiles = tiled_max_tiles(rows, gw.groups);
+      LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
+      LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, perm_tok, tiles, max_tiles, T, Imax, act, s));
       LBMOE_TRY(ev->mark(s));
       LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
-      LBMOE_TRY(launch_down_tiled_fp8(gw, actq, acts, Imax, counts, offsets, tiles, max_tiles, T,
-                                      out, s));
+      LBMOE_TRY(launch_down_tiled_fp8(gw, actq, acts, Imax, tiles, max_tiles, T, out, s));
     } else {
       LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, counts, offsets, perm_tok, T, k, Imax, act, s));
       LBMOE_TRY(ev->mark(s));
@@ -225,9 +219,8 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   if (use_tiled(gw, T, k)) {
     // prefill-sized batch: LDS-tiled MFMA GEMMs over a device-built token-tile list
     int32_t* tiles = at<int32_t>(ws, w, R_TILES);
-    const int max_tiles = tiled_max_tiles(T * k + (with_shared ? T : 0), gw.groups, kTilesBf16);
-    LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, kTilesBf16,
-                                 tiles, s));
+    const int max_tiles = tiled_max_tiles(T * k + (with_shared ? T : 0), gw.groups);
+    LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
     LBMOE_TRY(launch_gate_up_tiled(gw, x, perm_tok, tiles, max_tiles, T, Imax, act, s));
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_down_tiled(gw, act, Imax, tiles, max_tiles, T, out, s));

@@ -75,19 +75,18 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,
                           void* y, hipStream_t s);
-// LDS-tiled grouped GEMMs (prefill-sized batches). The bf16 kernels take a tile list of
-// wide and narrow token tiles, the fp8 kernels one of kFp8TileTokens-token tiles.
-enum TileListKind { kTilesBf16 = 0, kTilesFp8 = 1 };
-constexpr int kFp8TileTokens = 128;
+// LDS-tiled grouped GEMMs (prefill-sized batches) over a tile list of wide and narrow token
+// tiles, with one dispatch table per GEMM launch (bf16 and fp8 kernels share both).
 // Words behind a tile list's entries: count, wide count.
 constexpr int kTileListTail = 2;
-int tiled_max_tiles(int64_t rows, int groups, TileListKind kind);  // rows = routed + shared
-// Bytes of a bf16 tile list with max_tiles entries and the dispatch tables of both GEMMs.
+int tiled_max_tiles(int64_t rows, int groups);  // rows = routed + shared
+// Bytes of a tile list with max_tiles entries and the dispatch tables of both GEMMs.
 int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H);
 bool tiled_supported(const GroupWeights& gw);
+bool tiled_fp8_supported(const GroupWeights& gw);
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
-                              bool shared, int64_t T, int max_tiles, TileListKind kind,
-                              int32_t* tiles, hipStream_t s);
+                              bool shared, int64_t T, int max_tiles, int32_t* tiles,
+                              hipStream_t s);
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s);
@@ -95,13 +94,11 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
                              const int32_t* tiles, int max_tiles, int64_t T, void* out,
                              hipStream_t s);
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
-                                    const int32_t* counts, const int32_t* offsets,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
                                     int64_t T, int act_ld, void* act, hipStream_t s);
 hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const float* acts,
-                                 int act_ld, const int32_t* counts, const int32_t* offsets,
-                                 const int32_t* tiles, int max_tiles, int64_t T, void* out,
-                                 hipStream_t s);
+                                 int act_ld, const int32_t* tiles, int max_tiles, int64_t T,
+                                 void* out, hipStream_t s);
 bool tiled_router_supported(int E, int H);
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s);

@@ -1,146 +1,164 @@
 // LDS-tiled grouped GEMMs with fp8 (OCP e4m3) weights and activations, for prefill-sized
-// batches. They take a tile list of kFp8TileTokens-token tiles from build_tiles
-// (tiled_gemm.hip), deal its (token tile, weight tile) items to the XCDs in contiguous chunks
-// (xcd_item), and stage operands through a global->LDS ring; the products are those of the
-// fp8 streaming kernels (fp8.hip).
+// batches: the products of the fp8 streaming kernels (fp8.hip) on the tile geometry, tile list,
+// dispatch tables and global->LDS ring of the bf16 tiled GEMMs (tiled_shape.hpp,
+// tiled_gemm.hip).
 //
-// A k-stage is 128 k = 128 bytes per row = exactly one 128-k scale block, and one
-// v_mfma_scale_f32_16x16x128_f8f6f4 covers a 16 x 16 tile over the whole block (lane
-// (r, q) supplies bytes 32q .. 32q+31 of row r, OCP e4m3 operands, unit E8M0 scales). The
-// block product is scaled by w_scale(row block, k block) * a_scale(token, k block) and added
-// to the fp32 accumulator, so no partial sums need extra registers.
-// Workgroup: 4 waves in 2 x 2, tile kWM = 256 weight rows x kWT = 128 tokens; a wave owns
-// 128 rows (8 tiles of 16) x 64 tokens (4 tiles of 16). Accumulator lane (r, q) of a tile
-// holds token column r and rows 4q .. 4q+3, so four consecutive channels are stored together.
+// A k-tile is 128 bytes per row = 128 e4m3 values = exactly one 128-k scale block, so it has
+// the LDS geometry of a 64-value bf16 k-tile. One v_mfma_scale_f32_16x16x128_f8f6f4 covers a
+// 16 x 16 output tile over the whole k-tile (lane (r, q) supplies bytes 32q .. 32q+31 of row
+// r; OCP e4m3 operands, unit E8M0 scales). Its product p is scaled by
+// w_scale(row block, k-tile) * a_scale(token, k-tile) and added to the fp32 accumulator; the
+// fused multiply-adds of one MFMA step run under the next step's MFMAs.
+// Workgroup: 8 waves in 2 x 4, kWM = 256 weight rows x 256 tokens (wide: a wave owns 128 rows
+// x 64 tokens, 8 x 4 tiles of 16 x 16) or x 128 tokens (narrow: 128 x 32). Accumulator lane
+// (r, q) of a tile holds token column r and rows 4q .. 4q+3.
+// Scales live in LDS for the whole work item: the activation scales of the tile's tokens for
+// every k-tile (one 16-byte read per lane and k-tile) and the two weight-scale rows the
+// workgroup's rows use; both are copied global -> LDS ahead of the ring's first stage.
 #include "common.hpp"
 #include "internal.hpp"
-#include "tiled_common.hpp"
+#include "tiled_shape.hpp"
 
 namespace lbmoe {
 namespace f8t {
 
-typedef int i32x8_t __attribute__((ext_vector_type(8)));
+// The LDS ring of 128-byte k-tiles (TileShape counts k-tiles in bf16 units: BK = 64).
+using Wide = TileShape<2, 4, 2, 64, 2>;
+using Narrow = TileShape<2, 4, 1, 64, 2>;
+constexpr int kRingU4 = Wide::kStages * Wide::kStageU4;
+static_assert(Narrow::kStages * Narrow::kStageU4 <= kRingU4, "narrow ring exceeds the wide one");
+// Scale blocks per row (K / 128) the LDS scale area holds: K <= 3072.
+constexpr int kMaxKBlocks = 24;
+constexpr int kActScales = kMaxKBlocks * Wide::kWT;
+constexpr int kWScales = 64;                  // two rows of kMaxKBlocks, copied by one wave
+static_assert(2 * kMaxKBlocks <= kWScales, "weight-scale rows exceed one wave copy");
+static_assert(kRingU4 * 16 + (kActScales + kWScales) * 4 <= 160 * 1024, "LDS exceeds 160 KB");
 
-constexpr int kWM = 256;                 // weight rows per workgroup
-constexpr int kWT = kFp8TileTokens;     // tokens per workgroup (the fp8 tile list's width)
-constexpr int kBK = 128;                 // k (= bytes) per LDS stage
-constexpr int kStages = 3;
-constexpr int kWaves = 4;
-constexpr int kChunks = kBK / 16;        // 16-byte chunks per LDS row
-constexpr int kRowsPerLoad = 64 / kChunks;
-constexpr int kALoads = kWM / kRowsPerLoad / kWaves;
-constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;
-constexpr int kMT = kWM / 2 / 16;        // 16-row tiles per wave (weights)
-constexpr int kNT = kWT / 2 / 16;        // 16-column tiles per wave (tokens)
-constexpr int kStageU4 = (kWM + kWT) * kChunks;
-
-__device__ __forceinline__ int swz(int r, int j) { return r * kChunks + (j ^ ((r >> 1) & 7)); }
-
-__device__ __forceinline__ i32x8_t cat8(u32x4 lo, u32x4 hi) {
-  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+__device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+               (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
-template <bool GATEUP>
-__global__ __launch_bounds__(256) void tiled_fp8_kernel(
-    GroupWeights gw, const uint8_t* __restrict__ src, const float* __restrict__ src_scale,
-    int src_ld, const int32_t* __restrict__ offsets, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ perm_tok, const int32_t* __restrict__ tiles, int max_tiles,
-    int n_wtiles, int T, uint16_t* __restrict__ dst, int dst_ld) {
-  __shared__ u32x4 lds[kStages][kStageU4];
-  const int logical = xcd_item(blockIdx.x, tiles[2 * max_tiles] * n_wtiles);
-  if (logical < 0) return;
-  const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  const int g = tiles[2 * ti], r0 = tiles[2 * ti + 1];
+// Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g, output columns of weight tile wt.
+// GATEUP: act[row, c] = silu(gate) * up over K = H; else out[row, h] over K = Ig. row0: the
+// group's first row in src (down) / dst. src_sc: per (row, 128 k) activation scales, src_ld / 128
+// per row.
+template <bool GATEUP, class S>
+__device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
+                                                 const uint8_t* __restrict__ src,
+                                                 const float* __restrict__ src_sc, int src_ld,
+                                                 const int32_t* __restrict__ perm_tok, int g,
+                                                 int r0, int n, int row0, int wt,
+                                                 uint16_t* __restrict__ dst, int dst_ld,
+                                                 u32x4* __restrict__ lds, float* __restrict__ scl) {
+  constexpr int kM16 = 2 * S::kMT;               // 16-row tiles per wave
+  constexpr int kN16 = 2 * S::kNT;               // 16-token tiles per wave
+  constexpr int kRW = S::kRW, kWT = S::kWT, kWavesM = S::kWavesM;
+  constexpr int kStages = S::kStages, kChunks = S::kChunks, kRowsPerLoad = S::kRowsPerLoad;
+  constexpr int kALoads = S::kALoads, kBLoads = S::kBLoads, kLoads = S::kLoads;
+  constexpr int kStageU4 = S::kStageU4;
+  static_assert(kChunks == 8, "a k-tile is 128 bytes per row");
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int H = gw.H;
-  const int n = shared ? T : counts[g];
-  const int row0 = shared ? gw.sh_row0 : offsets[g];
-  const int K = GATEUP ? H : Ig;
-  const int nkb = K / 128;
-  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);
-  if (c0 >= (GATEUP ? Ig : H)) return;
+  const int K = GATEUP ? H : Ig;                 // bytes per weight row = k
+  const int nk = K / 128;                        // k-tiles = scale blocks
+  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);  // first channel / output column
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w & 1, wn = w >> 1;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = w % kWavesM, wn = w / kWavesM;
 
-  // weight rows, their block scales (rows of K/128 floats) and this thread's copy pointers
+  // Weights and the two weight-scale rows (nk floats each) of the workgroup's rows. gate_up:
+  // row 0 = the gate block of channels c0 .. c0+127, row 1 = their up block; down: the blocks
+  // of output columns c0 .. c0+127 and c0+128 .. c0+255 (wave row-block wm uses row wm).
   const uint8_t* wbase;
   const uint8_t* wup = nullptr;
-  const float* sw0;                      // scales of the wave's first (gate / down) block
-  const float* sw1;                      // scales of the wave's up block (gate_up only)
+  const float* sw0;
+  const float* sw1;
   if (GATEUP) {
     if (shared) {
       wbase = static_cast<const uint8_t*>(gw.sh_gate);
       wup = static_cast<const uint8_t*>(gw.sh_up);
-      sw0 = gw.sh_gate_scale + static_cast<int64_t>(c0 / 128) * nkb;
-      sw1 = gw.sh_up_scale + static_cast<int64_t>(c0 / 128) * nkb;
+      sw0 = gw.sh_gate_scale + static_cast<int64_t>(c0 / 128) * nk;
+      sw1 = gw.sh_up_scale + static_cast<int64_t>(c0 / 128) * nk;
     } else {
       wbase = static_cast<const uint8_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
       wup = wbase + static_cast<int64_t>(gw.I) * H;
-      const float* s0 = gw.gate_up_scale + static_cast<int64_t>(g) * (2 * gw.I / 128) * nkb;
-      sw0 = s0 + static_cast<int64_t>(c0 / 128) * nkb;
-      sw1 = s0 + static_cast<int64_t>((gw.I + c0) / 128) * nkb;
+      const float* s0 = gw.gate_up_scale + static_cast<int64_t>(g) * (2 * gw.I / 128) * nk;
+      sw0 = s0 + static_cast<int64_t>(c0 / 128) * nk;
+      sw1 = s0 + static_cast<int64_t>((gw.I + c0) / 128) * nk;
     }
   } else {
-    const int hb = (c0 + wm * (kWM / 2)) / 128;
     if (shared) {
       wbase = static_cast<const uint8_t*>(gw.sh_down);
-      sw0 = gw.sh_down_scale + static_cast<int64_t>(hb) * nkb;
+      sw0 = gw.sh_down_scale + static_cast<int64_t>(c0 / 128) * nk;
     } else {
       wbase = static_cast<const uint8_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
-      sw0 = gw.down_scale + (static_cast<int64_t>(g) * (H / 128) + hb) * nkb;
+      sw0 = gw.down_scale + (static_cast<int64_t>(g) * (H / 128) + c0 / 128) * nk;
     }
-    sw1 = sw0;
+    sw1 = sw0 + nk;
   }
+
+  // Ring copies, as in the bf16 kernels: wave copy i fills one 1 KB LDS block of kRowsPerLoad
+  // rows; lane l fetches the chunk that the swizzle places at slot l.
   const int lrow = lane / kChunks, lpos = lane % kChunks;
   const uint8_t* ap[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
     const int row = (w * kALoads + i) * kRowsPerLoad + lrow;
-    const int j = lpos ^ ((row >> 1) & 7);
+    const int j = lpos ^ ((row >> S::kSwzShift) & (kChunks - 1));
     const uint8_t* base = wbase;
     int grow;
     if (GATEUP) {
-      const int half = row / (kWM / 2), sub = row % (kWM / 2);
-      base = sub < kWM / 4 ? wbase : wup;
-      grow = c0 + half * (kWM / 4) + (sub % (kWM / 4));
+      const int half = row / kRW, sub = row % kRW;
+      base = sub < kRW / 2 ? wbase : wup;
+      grow = c0 + half * (kRW / 2) + (sub % (kRW / 2));
     } else {
       grow = c0 + row;
     }
     ap[i] = base + static_cast<int64_t>(grow) * K + 16 * j;
   }
+  auto src_row = [&](int lt) {         // source row of local token lt (past n: a valid row)
+    const int p = min(r0 + lt, n - 1);
+    return GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
+  };
   const uint8_t* bp[kBLoads];
 #pragma unroll
   for (int i = 0; i < kBLoads; ++i) {
     const int lt = (w * kBLoads + i) * kRowsPerLoad + lrow;
     const int row = kWM + lt;
-    const int j = lpos ^ ((row >> 1) & 7);
-    const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
-    const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
-    bp[i] = src + static_cast<int64_t>(srow) * src_ld + 16 * j;
+    const int j = lpos ^ ((row >> S::kSwzShift) & (kChunks - 1));
+    bp[i] = src + static_cast<int64_t>(src_row(lt)) * src_ld + 16 * j;
   }
-  // activation scale rows of this lane's accumulator columns
-  const int r = lane & 15, q = lane >> 4;
-  const int sa_ld = src_ld / 128;
-  const float* sap[kNT];
-#pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    const int p = min(r0 + wn * (kWT / 2) + 16 * t + r, n - 1);
-    const int srow = GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
-    sap[t] = src_scale + static_cast<int64_t>(srow) * sa_ld;
-  }
-
-  f32x4 acc[kMT][kNT];
-#pragma unroll
-  for (int i = 0; i < kMT; ++i)
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
+  // Scale copies (4 bytes per lane). Activation scales: scl[kb * kWT + pos], pos =
+  // wn' * 16 kN16 + r * kN16 + t for local token wn' * 16 kN16 + 16 t + r, so that a lane
+  // reads its kN16 columns' scales of one k-tile with one load. Wave w copies 64-entry block
+  // w % nb of k-tiles w / nb, w / nb + 8 / nb, ...; wave 0 also copies the weight-scale rows.
+  {
+    constexpr int nb = kWT / 64;
+    const int pos = (w % nb) * 64 + lane;
+    const int lt = (pos / (16 * kN16)) * (16 * kN16) + 16 * (pos % kN16) + (pos % (16 * kN16)) / kN16;
+    const float* sp = src_sc + static_cast<int64_t>(src_row(lt)) * (src_ld / 128);
+    for (int kb = w / nb; kb < nk; kb += kWaves / nb)
+      __builtin_amdgcn_global_load_lds(sp + kb, (lds_ptr)(scl + kb * kWT + (w % nb) * 64), 4, 0, 0);
+    if (w == 0) {
+      const float* wsp = lane < nk ? sw0 + lane : (lane < 2 * nk ? sw1 + (lane - nk) : sw0);
+      __builtin_amdgcn_global_load_lds(wsp, (lds_ptr)(scl + kActScales), 4, 0, 0);
+    }
+  }
+  const float* wsc = scl + kActScales;
+
+  f32x4 acc[kM16][kN16];
+#pragma unroll
+  for (int i = 0; i < kM16; ++i)
+#pragma unroll
+    for (int t = 0; t < kN16; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
   auto issue = [&](int stage, int k0) {
-    u32x4* buf = lds[stage];
+    u32x4* buf = lds + stage * kStageU4;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
       __builtin_amdgcn_global_load_lds(ap[i] + k0,
@@ -148,91 +166,160 @@ __global__ __launch_bounds__(256) void tiled_fp8_kernel(
                                        16, 0, 0);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
-      __builtin_amdgcn_global_load_lds(
-          bp[i] + k0, (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(bp[i] + k0,
+                                       (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
+                                       16, 0, 0);
   };
 
-  const int nk = K / kBK;
+  const int r16 = lane & 15, q = lane >> 4;
+  auto read_a = [&](const u32x4* buf, int i) {
+    const int row = wm * kRW + 16 * i + r16;
+    return cat8(buf[S::swz(row, 2 * q)], buf[S::swz(row, 2 * q + 1)]);
+  };
+  auto read_b = [&](const u32x4* buf, int t) {
+    const int row = kWM + wn * (16 * kN16) + 16 * t + r16;
+    return cat8(buf[S::swz(row, 2 * q)], buf[S::swz(row, 2 * q + 1)]);
+  };
+  // Ring protocol of the bf16 kernels: all kStages buffers are filled up front; in k-tile kt,
+  // once the last A tile's fragments are in registers, each wave waits for its copies of
+  // stage kt+1 and meets the others at the barrier, then reads stage kt+1's B fragments and
+  // first A fragment and refills stage kt's buffer, interleaved with the last MFMAs.
 #pragma unroll
-  for (int st = 0; st < kStages - 1; ++st)
-    if (st < nk) issue(st, st * kBK);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_ring<kStages - 2, kALoads + kBLoads>(nk - 1 - kt);
-    ring_barrier();
-    if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, (kt + kStages - 1) * kBK);
-    const u32x4* cur = lds[kt % kStages];
-    const float s_gate = sw0[kt], s_up = sw1[kt];
-    float sa[kNT];
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) sa[t] = sap[t][kt];
-    i32x8_t fb[kNT];
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int row = kWM + wn * (kWT / 2) + 16 * t + r;
-      fb[t] = cat8(cur[swz(row, 2 * q)], cur[swz(row, 2 * q + 1)]);
-    }
-#pragma unroll
-    for (int i = 0; i < kMT; ++i) {
-      const int row = wm * (kWM / 2) + 16 * i + r;
-      const i32x8_t fa = cat8(cur[swz(row, 2 * q)], cur[swz(row, 2 * q + 1)]);
-      const float sw = (GATEUP && i >= kMT / 2) ? s_up : s_gate;
-#pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            fa, fb[t], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        acc[i][t] += p * (sw * sa[t]);
-      }
-    }
-  }
+  for (int st = 0; st < kStages; ++st)
+    if (st < nk) issue(st, st * 128);
+  wait_ring<kStages - 1, kLoads>(nk - 1);
+  ring_barrier();
 
-  // Epilogue.
+  i32x8 fa[2], fb[kN16];
+  f32x4 p[kN16];            // products of the previous MFMA step, not yet scaled and added
+  float sp[kN16];           // their scales
 #pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    const int p = r0 + wn * (kWT / 2) + 16 * t + r;
-    if (p >= n) continue;
-    uint16_t* orow = dst + static_cast<int64_t>(row0 + p) * dst_ld;
-    if (GATEUP) {
+  for (int t = 0; t < kN16; ++t) {
+    fb[t] = read_b(lds, t);
+    p[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sp[t] = 0.f;
+  }
+  fa[0] = read_a(lds, 0);
+
+  auto ktile = [&]<bool NEXT, bool REFILL>(int kt) {
+    const u32x4* cur = lds + (kt % kStages) * kStageU4;
+    // this k-tile's scales: s[h][t] = weight scale h * activation scale of column t, h = 0 for
+    // gate and down tiles, 1 for up tiles
+    float sa[kN16];
+    {
+      const float* a = scl + kt * kWT + wn * (16 * kN16) + r16 * kN16;
 #pragma unroll
-      for (int i = 0; i < kMT / 2; ++i) {
-        float a[4];
+      for (int t = 0; t < kN16; ++t) sa[t] = a[t];
+    }
+    const float w0 = wsc[(GATEUP ? 0 : wm) * nk + kt];
+    const float w1 = GATEUP ? wsc[nk + kt] : w0;
+    float s[2][kN16];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) a[v] = silu(acc[i][t][v]) * acc[i + kMT / 2][t][v];
-        const int ch = c0 + wm * (kWM / 4) + 16 * i + 4 * q;
-        *reinterpret_cast<u32x2*>(orow + ch) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+    for (int t = 0; t < kN16; ++t) {
+      s[0][t] = w0 * sa[t];
+      s[1][t] = w1 * sa[t];
+    }
+#pragma unroll
+    for (int i = 0; i < kM16; ++i) {
+      const bool last = i == kM16 - 1;
+      // the pending products belong to the previous step (at i = 0: the previous k-tile's
+      // last step, or zeros with zero scales before the first k-tile)
+      const int pi = i == 0 ? kM16 - 1 : i - 1;
+      const int h = GATEUP && i >= kM16 / 2 ? 1 : 0;
+      if (!last) fa[(i + 1) & 1] = read_a(cur, i + 1);
+      if (last && NEXT) {
+        // every earlier MFMA stays above the barrier
+        __builtin_amdgcn_sched_barrier(0);
+        wait_ring<kStages - 2, kLoads>(nk - 2 - kt);
+        ring_barrier();
       }
-    } else {
+      const u32x4* nxt = lds + ((kt + 1) % kStages) * kStageU4;
 #pragma unroll
-      for (int i = 0; i < kMT; ++i) {
-        const int h = c0 + wm * (kWM / 2) + 16 * i + 4 * q;
-        *reinterpret_cast<u32x2*>(orow + h) =
-            u32x2{pack_bf2(acc[i][t][0], acc[i][t][1]), pack_bf2(acc[i][t][2], acc[i][t][3])};
+      for (int t = 0; t < kN16; ++t) {
+        acc[pi][t] += p[t] * sp[t];
+        p[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            fa[i & 1], fb[t], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+        sp[t] = s[h][t];
+        if (last && NEXT) fb[t] = read_b(nxt, t);
+      }
+      if (last && NEXT) {
+        fa[0] = read_a(nxt, 0);
+        if constexpr (REFILL) issue(kt % kStages, (kt + kStages) * 128);
       }
     }
+  };
+  int kt = 0;
+  for (; kt + kStages < nk; ++kt) ktile.template operator()<true, true>(kt);
+  for (; kt + 1 < nk; ++kt) ktile.template operator()<true, false>(kt);
+  ktile.template operator()<false, false>(kt);
+#pragma unroll
+  for (int t = 0; t < kN16; ++t) acc[kM16 - 1][t] += p[t] * sp[t];
+
+  // Epilogue: stage the tile in the ring as [token][column] bf16, then store row segments.
+  constexpr int kCols = GATEUP ? kWM / 2 : kWM;
+  static_assert(kWT * (kCols / 8) <= kRingU4, "staged tile exceeds the LDS ring");
+  ring_barrier();                                           // every wave is done with the ring
+  char* st = reinterpret_cast<char*>(lds);
+#pragma unroll
+  for (int t = 0; t < kN16; ++t) {
+    const int r = wn * (16 * kN16) + 16 * t + r16;          // token within the tile
+#pragma unroll
+    for (int i = 0; i < (GATEUP ? kM16 / 2 : kM16); ++i) {
+      float a[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        a[v] = GATEUP ? silu(acc[i][t][v]) * acc[i + kM16 / 2][t][v] : acc[i][t][v];
+      const int c = (GATEUP ? wm * (kRW / 2) : wm * kRW) + 16 * i + 4 * q;
+      *reinterpret_cast<u32x2*>(st + staged_slot<kCols>(r, c / 8) * 16 + (c % 8) * 2) =
+          u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+    }
   }
+  ring_barrier();
+  store_staged<kCols, kWT>(lds, dst, dst_ld, row0, r0, n, c0);
+}
+
+template <bool GATEUP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
+                      const float* __restrict__ src_sc, int src_ld,
+                      const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table,
+                      uint16_t* __restrict__ dst, int dst_ld) {
+  __shared__ u32x4 lds[kRingU4];
+  __shared__ float scl[kActScales + kWScales];
+  const TileItem it = decode_item(table[blockIdx.x]);
+  if (it.g < 0) return;
+  if (it.narrow)
+    tile_product_fp8<GATEUP, Narrow>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                     it.row0, it.wt, dst, dst_ld, lds, scl);
+  else
+    tile_product_fp8<GATEUP, Wide>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                   it.row0, it.wt, dst, dst_ld, lds, scl);
 }
 
 }  // namespace f8t
 
+bool tiled_fp8_supported(const GroupWeights& gw) {
+  return tiled_supported(gw) && gw.H / 128 <= f8t::kMaxKBlocks &&
+         gw.I / 128 <= f8t::kMaxKBlocks && gw.Is / 128 <= f8t::kMaxKBlocks;
+}
+
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
-                                    const int32_t* counts, const int32_t* offsets,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
                                     int64_t T, int act_ld, void* act, hipStream_t s) {
-  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const int n_wtiles = Imax / (f8t::kWM / 2);
-  f8t::tiled_fp8_kernel<true><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
-      gw, static_cast<const uint8_t*>(xq), xs, gw.H, offsets, counts, perm_tok, tiles, max_tiles,
-      n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
+  (void)T;
+  f8t::tiled_fp8_kernel<true><<<tiled_grid(gw, max_tiles, true), kThreads, 0, s>>>(
+      gw, static_cast<const uint8_t*>(xq), xs, gw.H, perm_tok,
+      tiled_table(gw, tiles, max_tiles, true), static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
 }
 
 hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const float* acts,
-                                 int act_ld, const int32_t* counts, const int32_t* offsets,
-                                 const int32_t* tiles, int max_tiles, int64_t T, void* out,
-                                 hipStream_t s) {
-  const int n_wtiles = gw.H / f8t::kWM;
-  f8t::tiled_fp8_kernel<false><<<round8(static_cast<int64_t>(max_tiles) * n_wtiles), 256, 0, s>>>(
-      gw, static_cast<const uint8_t*>(actq), acts, act_ld, offsets, counts, nullptr, tiles,
-      max_tiles, n_wtiles, static_cast<int>(T), static_cast<uint16_t*>(out), gw.H);
+                                 int act_ld, const int32_t* tiles, int max_tiles, int64_t T,
+                                 void* out, hipStream_t s) {
+  (void)T;
+  f8t::tiled_fp8_kernel<false><<<tiled_grid(gw, max_tiles, false), kThreads, 0, s>>>(
+      gw, static_cast<const uint8_t*>(actq), acts, act_ld, nullptr,
+      tiled_table(gw, tiles, max_tiles, false), static_cast<uint16_t*>(out), gw.H);
   return hipGetLastError();
 }
 

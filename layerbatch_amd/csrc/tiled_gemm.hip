@@ -31,13 +31,9 @@
 // then the up rows of the same channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
 #include "internal.hpp"
-#include "tiled_common.hpp"
+#include "tiled_shape.hpp"
 
 namespace lbmoe {
-
-constexpr int kWaves = 8;                           // two waves per SIMD
-constexpr int kThreads = 64 * kWaves;
-constexpr int kWM = 256;                            // weight rows per workgroup
 
 #ifndef LBMOE_TILE_BK
 #define LBMOE_TILE_BK 64
@@ -52,38 +48,6 @@ constexpr int kWM = 256;                            // weight rows per workgroup
 #define LBMOE_NARROW_STAGES 3
 #endif
 
-// One token-tile shape: WAVES_M x (kWaves / WAVES_M) waves, each owning MT x NT 32x32 MFMA
-// tiles (weights x tokens), k-tiles of BK, STAGES LDS buffers.
-template <int WAVES_M, int MT, int NT, int BK, int STAGES>
-struct TileShape {
-  static constexpr int kWavesM = WAVES_M;
-  static constexpr int kWavesN = kWaves / WAVES_M;
-  static constexpr int kMT = MT;
-  static constexpr int kNT = NT;
-  static constexpr int kRW = MT * 32;                         // weight rows per wave
-  static constexpr int kWT = kWavesN * NT * 32;               // tokens per workgroup
-  static constexpr int kBK = BK;
-  static constexpr int kStages = STAGES;
-  static constexpr int kChunks = BK / 8;                      // 16-byte chunks per LDS row
-  static constexpr int kRowsPerLoad = 64 / kChunks;           // rows one wave copy covers
-  static constexpr int kALoads = kWM / kRowsPerLoad / kWaves;  // wave copies per stage (weights)
-  static constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;  // wave copies per stage (tokens)
-  static constexpr int kLoads = kALoads + kBLoads;
-  static constexpr int kStageU4 = (kWM + kWT) * kChunks;      // 16-byte slots per stage
-  static constexpr int kKSteps = BK / 16;                     // MFMA k-steps per k-tile
-  // Chunk j of row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
-  // kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
-  static constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
-  static_assert(WAVES_M * MT * 32 == kWM, "waves must tile the weight rows");
-  static_assert(kChunks == 4 || kChunks == 8, "BK must be 32 or 64");
-  static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
-                "copies must tile the stage");
-  static_assert(kKSteps % 2 == 0, "the next k-tile's first fragments go to register buffer 0");
-  static_assert(MT % 2 == 0, "gate_up pairs a wave's gate tiles with its up tiles");
-  static __device__ __forceinline__ int swz(int r, int j) {
-    return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
-  }
-};
 // wide: 2 x 4 waves of 128 x 64 (256 tokens); narrow: 2 x 4 waves of 128 x 32 (128 tokens)
 using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
 using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
@@ -94,8 +58,6 @@ constexpr int kLdsU4 = Wide::kStages * Wide::kStageU4 > Narrow::kStages * Narrow
                            : Narrow::kStages * Narrow::kStageU4;
 static_assert(RouterShape::kStages * RouterShape::kStageU4 <= kLdsU4, "router ring too large");
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
-
-constexpr int32_t kNarrowFlag = 1 << 30;
 
 // ---- tile list -------------------------------------------------------------------------------
 // tiles[2i] = group, tiles[2i+1] = first row within the group (| kNarrowFlag for a narrow
@@ -441,13 +403,9 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   if constexpr (!ROUTER) {
     // Stage the tile in LDS as row-major [token][column] bf16, then store whole row segments
     // (kCols * 2 contiguous bytes per token) with 16-byte lanes. Storing straight from the
-    // accumulators would write 16-byte pieces of 32 token rows per instruction. 16-byte chunk
-    // c of staged row r sits at chunk c ^ (r mod kRowChunks), which spreads the 32 rows of an
-    // accumulator write over distinct banks.
+    // accumulators would write 16-byte pieces of 32 token rows per instruction.
     constexpr int kCols = GATEUP ? kWM / 2 : kWM;            // output columns per tile
-    constexpr int kRowChunks = kCols / 8;
-    static_assert(S::kWT * kRowChunks <= kLdsU4, "staged tile exceeds the LDS ring");
-    auto slot = [&](int r, int c) { return r * kRowChunks + (c ^ (r & (kRowChunks - 1))); };
+    static_assert(S::kWT * (kCols / 8) <= kLdsU4, "staged tile exceeds the LDS ring");
     ring_barrier();                                           // every wave is done with the ring
     char* st = reinterpret_cast<char*>(lds);
 #pragma unroll
@@ -463,19 +421,12 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
             a[v] = GATEUP ? silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v]
                           : acc[i][t][4 * v4 + v];
           const int c = (GATEUP ? wm * (kRW / 2) : wm * kRW) + 32 * i + 8 * v4 + rq;
-          *reinterpret_cast<u32x2*>(st + slot(r, c / 8) * 16 + (c % 8) * 2) =
+          *reinterpret_cast<u32x2*>(st + staged_slot<kCols>(r, c / 8) * 16 + (c % 8) * 2) =
               u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
     }
     ring_barrier();
-    constexpr int kRowsPerPass = kThreads / kRowChunks;
-    const int c = threadIdx.x % kRowChunks;
-    for (int r = threadIdx.x / kRowChunks; r < S::kWT; r += kRowsPerPass) {
-      const int p = r0 + r;
-      if (p >= n) break;
-      *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(row0 + p) * dst_ld + c0 + 8 * c) =
-          lds[slot(r, c)];
-    }
+    store_staged<kCols, S::kWT>(lds, dst, dst_ld, row0, r0, n, c0);
   } else {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
@@ -521,36 +472,22 @@ void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
                   const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table, int T,
                   uint16_t* __restrict__ dst, int dst_ld) {
   __shared__ u32x4 lds[kLdsU4];
-  const u32x4 ent = table[blockIdx.x];
-  const int gx = static_cast<int>(ent[0]);
-  if (gx < 0) return;
-  const int g = gx & 0xffff, wt = gx >> 16, e = static_cast<int>(ent[1]);
-  const int row0 = static_cast<int>(ent[2]), n = static_cast<int>(ent[3]);
-  if (e & kNarrowFlag)
-    tile_product<MODE, Narrow>(gw, src, src_ld, perm_tok, g, e & (kNarrowFlag - 1), n, row0, wt,
+  const TileItem it = decode_item(table[blockIdx.x]);
+  if (it.g < 0) return;
+  if (it.narrow)
+    tile_product<MODE, Narrow>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n, it.row0, it.wt,
                                dst, dst_ld, lds);
   else
-    tile_product<MODE, Wide>(gw, src, src_ld, perm_tok, g, e, n, row0, wt, dst, dst_ld, lds);
+    tile_product<MODE, Wide>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n, it.row0, it.wt, dst,
+                             dst_ld, lds);
 }
 
 // ---- host side -------------------------------------------------------------------------------
-static void tile_widths(TileListKind kind, int& wide, int& narrow) {
-  if (kind == kTilesFp8) {
-    wide = kFp8TileTokens;
-    narrow = 0;
-  } else {
-    wide = Wide::kWT;
-    narrow = Narrow::kWT;
-  }
-}
-
 // Upper bound of the tile-list length: rows / wide full tiles, plus per group at most one
 // partial wide tile or (wide - narrow) / narrow narrow tiles.
-int tiled_max_tiles(int64_t rows, int groups, TileListKind kind) {
-  int wide, narrow;
-  tile_widths(kind, wide, narrow);
-  const int per_group = narrow == 0 ? 1 : (wide - narrow) / narrow;
-  return static_cast<int>(rows / wide) + groups * per_group + 1;
+int tiled_max_tiles(int64_t rows, int groups) {
+  static_assert(Wide::kWT % Narrow::kWT == 0, "narrow tiles divide wide ones");
+  return static_cast<int>(rows / Wide::kWT) + groups * ((Wide::kWT - Narrow::kWT) / Narrow::kWT) + 1;
 }
 
 bool tiled_supported(const GroupWeights& gw) {
@@ -574,37 +511,42 @@ int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H) {
   return table_base(max_tiles) * 4 + slots * 16;
 }
 
+int tiled_grid(const GroupWeights& gw, int max_tiles, bool gate_up) {
+  return item_grid(max_tiles, gate_up ? gate_up_wtiles(gw.I, gw.Is) : down_wtiles(gw.H));
+}
+
+const u32x4* tiled_table(const GroupWeights& gw, const int32_t* tiles, int max_tiles,
+                         bool gate_up) {
+  const auto* t = reinterpret_cast<const u32x4*>(tiles + table_base(max_tiles));
+  return gate_up ? t : t + tiled_grid(gw, max_tiles, true);
+}
+
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
-                              bool shared, int64_t T, int max_tiles, TileListKind kind,
-                              int32_t* tiles, hipStream_t s) {
-  int wide, narrow;
-  tile_widths(kind, wide, narrow);
-  const bool tables = kind == kTilesBf16;
-  const int grid_gu = tables ? item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is)) : 0;
-  const int grid_dn = tables ? item_grid(max_tiles, down_wtiles(gw.H)) : 0;
+                              bool shared, int64_t T, int max_tiles, int32_t* tiles,
+                              hipStream_t s) {
   build_tiles_kernel<<<1, 1024, 0, s>>>(counts, offsets, gw.E, shared ? 1 : 0,
-                                        static_cast<int>(T), gw.sh_row0, max_tiles, wide, narrow,
-                                        gw.I, gw.Is, gw.H, grid_gu, grid_dn, tiles);
+                                        static_cast<int>(T), gw.sh_row0, max_tiles, Wide::kWT,
+                                        Narrow::kWT, gw.I, gw.Is, gw.H,
+                                        tiled_grid(gw, max_tiles, true),
+                                        tiled_grid(gw, max_tiles, false), tiles);
   return hipGetLastError();
 }
 
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s) {
-  const auto* table = reinterpret_cast<const u32x4*>(tiles + table_base(max_tiles));
-  tiled_kernel<kGateUp><<<item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is)), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(x), gw.H, perm_tok, table, static_cast<int>(T),
-      static_cast<uint16_t*>(act), act_ld);
+  tiled_kernel<kGateUp><<<tiled_grid(gw, max_tiles, true), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), gw.H, perm_tok, tiled_table(gw, tiles, max_tiles, true),
+      static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
   return hipGetLastError();
 }
 
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
                              const int32_t* tiles, int max_tiles, int64_t T, void* out,
                              hipStream_t s) {
-  const auto* table = reinterpret_cast<const u32x4*>(tiles + table_base(max_tiles)) +
-                      item_grid(max_tiles, gate_up_wtiles(gw.I, gw.Is));
-  tiled_kernel<kDown><<<item_grid(max_tiles, down_wtiles(gw.H)), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(act), act_ld, nullptr, table, static_cast<int>(T),
+  tiled_kernel<kDown><<<tiled_grid(gw, max_tiles, false), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(act), act_ld, nullptr,
+      tiled_table(gw, tiles, max_tiles, false), static_cast<int>(T),
       static_cast<uint16_t*>(out), gw.H);
   return hipGetLastError();
 }
