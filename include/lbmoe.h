@@ -90,7 +90,8 @@ int32_t lbmoe_workspace_size(const lbmoe_layer* layer, int64_t T, size_t* bytes)
  * inspection of intermediates after lbmoe_forward. region: 0 logits bf16 [T,E],
  * 1 topk_idx int32 [T,k], 2 topk_w bf16 [T,k], 3 shared_gate fp32 [T],
  * 4 counts int32 [E+1], 5 offsets int32 [E+2], 6 perm_tok int32 [T*k+T],
- * 7 perm_slot int32 [T*k], 8 inv int32 [T,k], 9 act [T*k+T, max(I,Is)],
+ * 7 perm_slot int32 [T*k], 8 inv int32 [T,k], 9 act bf16 [T*k+T, max(I,Is)]
+ * (not written by the fp8 prefill path, whose gate_up stores the quantised act directly),
  * 10 expert_out bf16 [T*k+T, H]. */
 int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t region,
                                size_t* offset, size_t* bytes);

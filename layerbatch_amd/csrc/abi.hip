@@ -201,10 +201,10 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
       int32_t* tiles = at<int32_t>(ws, w, R_TILES);
       const int max_tiles = tiled_max_tiles(rows, gw.groups);
       LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
-      LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, perm_tok, tiles, max_tiles, T, Imax, act, s));
+      LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, perm_tok, tiles, max_tiles, Imax, actq, acts,
+                                         s));
       LBMOE_TRY(ev->mark(s));
-      LBMOE_TRY(launch_quant_groups_fp8(act, rows, Imax, Imax, actq, acts, s));
-      LBMOE_TRY(launch_down_tiled_fp8(gw, actq, acts, Imax, tiles, max_tiles, T, out, s));
+      LBMOE_TRY(launch_down_tiled_fp8(gw, actq, acts, Imax, tiles, max_tiles, out, s));
     } else {
       LBMOE_TRY(launch_gate_up_fp8(gw, xq, xs, counts, offsets, perm_tok, T, k, Imax, act, s));
       LBMOE_TRY(ev->mark(s));

@@ -36,41 +36,37 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
 __device__ __forceinline__ float round_bf(float f) { return __uint_as_float(f2bf(f) << 16); }
 
 // ---- OCP e4m3fn ----------------------------------------------------------------------------
-// Round-to-nearest-even, saturating to +-448; NaN -> 0x7f. Values are quantised from
-// x / scale with |x / scale| <= 448 up to rounding, so saturation only trims ulps.
-__device__ __forceinline__ uint32_t f2e4m3(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t sign = (u >> 24) & 0x80u;
-  float a = fabsf(f);
-  if (!(a == a)) return 0x7fu;
-  if (a >= 448.0f) return sign | 0x7eu;
-  uint32_t ua = __float_as_uint(a);
-  int e = static_cast<int>(ua >> 23) - 127;              // unbiased exponent of a
-  uint32_t code;
-  if (e < -6) {
-    // subnormal range: value = m * 2^-9, m in [0,8]; RNE of a * 2^9
-    float m = a * 512.0f;                                // exact (power-of-two scale)
-    float r = rintf(m);                                  // round half to even
-    code = static_cast<uint32_t>(r);                     // 8 -> 0x08 = smallest normal
-  } else {
-    // normal: keep 3 mantissa bits with RNE on the fp32 mantissa
-    uint32_t mant = ua & 0x7fffffu;
-    uint32_t keep = mant >> 20;
-    uint32_t rest = mant & 0xfffffu;
-    uint32_t half = 0x80000u;
-    uint32_t q = (static_cast<uint32_t>(e + 7) << 3) | keep;
-    if (rest > half || (rest == half && (keep & 1u))) q += 1;  // carry may bump exponent
-    code = q;
-    if (code > 0x7eu) code = 0x7eu;
-  }
-  return sign | code;
+// Round-to-nearest-even (v_cvt_pk_fp8_f32), subnormals included. Values are quantised from
+// x / scale with scale = amax / 448, so |x / scale| exceeds 448 by at most rounding and rounds
+// to +-448. Four values -> four codes, a in the low byte.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
 }
 
-__device__ __forceinline__ float e4m3_to_f(uint32_t c) {
-  uint32_t s = c & 0x80u, e = (c >> 3) & 0xfu, m = c & 7u;
-  float v = (e == 0) ? static_cast<float>(m) * (1.0f / 512.0f)
-                     : __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return s ? -v : v;
+// Activation quantisation (per row and 128 channels): scale = amax / 448, 1 for an all-zero
+// group; code = e4m3(value / scale). One group is held by 16 consecutive lanes of a wave
+// (lanes 16j .. 16j+15), 8 channels per lane as 8 bf16 in v; every lane of the group must be
+// active. Returns the lane's 8 codes; s receives the group's scale.
+__device__ __forceinline__ float fp8_scale_of(float amax) { return amax > 0.f ? amax / 448.0f : 1.0f; }
+__device__ __forceinline__ u32x2 quant_group16(u32x4 v, float& s) {
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bf_lo(v[j]);
+    x[2 * j + 1] = bf_hi(v[j]);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  s = fp8_scale_of(amax);
+  u32x2 c;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    c[h] = e4m3x4(x[4 * h] / s, x[4 * h + 1] / s, x[4 * h + 2] / s, x[4 * h + 3] / s);
+  return c;
 }
 
 // ---- wave reductions --------------------------------------------------------------------

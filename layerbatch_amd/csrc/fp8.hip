@@ -7,8 +7,6 @@
 
 namespace lbmoe {
 
-__device__ __forceinline__ float scale_of(float amax) { return amax > 0.f ? amax / 448.0f : 1.0f; }
-
 // One 256-thread workgroup per 128x128 block; thread i covers row i/2, 64 columns.
 __global__ __launch_bounds__(256) void quant_blocks_kernel(const uint16_t* __restrict__ w,
                                                            int N, int K,
@@ -35,7 +33,7 @@ __global__ __launch_bounds__(256) void quant_blocks_kernel(const uint16_t* __res
   if (lane_id() == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = scale_of(amax);
+  const float s = fp8_scale_of(amax);
   if (threadIdx.x == 0) scale[blk] = s;
 #pragma unroll
   for (int i = 0; i < 8; i += 2) {
@@ -45,8 +43,7 @@ __global__ __launch_bounds__(256) void quant_blocks_kernel(const uint16_t* __res
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const uint32_t lo = v[i + h][2 * j], hi = v[i + h][2 * j + 1];
-        o[2 * h + j] = f2e4m3(bf_lo(lo) / s) | (f2e4m3(bf_hi(lo) / s) << 8) |
-                       (f2e4m3(bf_lo(hi) / s) << 16) | (f2e4m3(bf_hi(hi) / s) << 24);
+        o[2 * h + j] = e4m3x4(bf_lo(lo) / s, bf_hi(lo) / s, bf_lo(hi) / s, bf_hi(hi) / s);
       }
     }
     *reinterpret_cast<u32x4*>(q + base + 8 * i) = o;
@@ -61,31 +58,31 @@ hipError_t launch_quant_blocks_fp8(const void* w, int64_t batch, int N, int K, v
   return hipGetLastError();
 }
 
-// One wave per (row, 128-channel group); lane i covers channels 2i, 2i+1.
+// 16 lanes per (row, 128-channel group), 8 channels per lane (16-byte loads, 8-byte stores);
+// the group's amax is reduced over its 16 lanes.
+constexpr int kGroupsPerBlock = 16;
 __global__ __launch_bounds__(256) void quant_groups_kernel(const uint16_t* __restrict__ a,
                                                            int64_t rows, int cols, int ld,
                                                            uint8_t* __restrict__ q,
                                                            float* __restrict__ scale) {
   const int ng = cols / 128;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + (threadIdx.x >> 4);
   if (gid >= rows * ng) return;
   const int64_t row = gid / ng;
   const int grp = static_cast<int>(gid - row * ng);
-  const int lane = lane_id();
-  const uint32_t v = *reinterpret_cast<const uint32_t*>(a + row * ld + grp * 128 + 2 * lane);
-  const float x0 = bf_lo(v), x1 = bf_hi(v);
-  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const float s = scale_of(amax);
-  if (lane == 0) scale[row * ng + grp] = s;
-  const uint32_t c = f2e4m3(x0 / s) | (f2e4m3(x1 / s) << 8);
-  *reinterpret_cast<uint16_t*>(q + row * cols + grp * 128 + 2 * lane) = static_cast<uint16_t>(c);
+  const int sub = threadIdx.x & 15;
+  float sc;
+  const u32x2 c = quant_group16(ld16(a + row * ld + grp * 128 + 8 * sub), sc);
+  if (sub == 0) scale[row * ng + grp] = sc;
+  *reinterpret_cast<u32x2*>(q + row * cols + grp * 128 + 8 * sub) = c;
 }
 
 hipError_t launch_quant_groups_fp8(const void* a, int64_t rows, int cols, int ld, void* q,
                                    float* scale, hipStream_t s) {
-  const int64_t waves = rows * (cols / 128);
-  if (waves == 0) return hipSuccess;
-  quant_groups_kernel<<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(
+  const int64_t groups = rows * (cols / 128);
+  if (groups == 0) return hipSuccess;
+  quant_groups_kernel<<<static_cast<unsigned>((groups + kGroupsPerBlock - 1) / kGroupsPerBlock),
+                        256, 0, s>>>(
       static_cast<const uint16_t*>(a), rows, cols, ld, static_cast<uint8_t*>(q), scale);
   return hipGetLastError();
 }

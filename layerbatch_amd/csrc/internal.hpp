@@ -93,12 +93,14 @@ hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
                              const int32_t* tiles, int max_tiles, int64_t T, void* out,
                              hipStream_t s);
+// fp8: gate_up writes the quantised act (e4m3 codes, act_ld bytes per row, and per (row, 128)
+// scales) that down reads.
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
-                                    int64_t T, int act_ld, void* act, hipStream_t s);
+                                    int act_ld, void* actq, float* acts, hipStream_t s);
 hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const float* acts,
-                                 int act_ld, const int32_t* tiles, int max_tiles, int64_t T,
-                                 void* out, hipStream_t s);
+                                 int act_ld, const int32_t* tiles, int max_tiles, void* out,
+                                 hipStream_t s);
 bool tiled_router_supported(int E, int H);
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s);

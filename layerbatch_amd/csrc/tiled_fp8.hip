@@ -40,16 +40,19 @@ __device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
 }
 
 // Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g, output columns of weight tile wt.
-// GATEUP: act[row, c] = silu(gate) * up over K = H; else out[row, h] over K = Ig. row0: the
-// group's first row in src (down) / dst. src_sc: per (row, 128 k) activation scales, src_ld / 128
-// per row.
+// GATEUP: act[row, c] = silu(gate) * up over K = H, rounded to bf16 and quantised for the down
+// GEMM: the tile's 128 channels are one quantisation group, so dst receives the e4m3 codes
+// (dst_ld bytes per row) and dst_sc the group scales (dst_ld / 128 per row). Else out[row, h]
+// (bf16, dst_ld per row) over K = Ig. row0: the group's first row in src (down) / dst. src_sc:
+// per (row, 128 k) activation scales of src, src_ld / 128 per row.
 template <bool GATEUP, class S>
 __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
                                                  const uint8_t* __restrict__ src,
                                                  const float* __restrict__ src_sc, int src_ld,
                                                  const int32_t* __restrict__ perm_tok, int g,
                                                  int r0, int n, int row0, int wt,
-                                                 uint16_t* __restrict__ dst, int dst_ld,
+                                                 void* __restrict__ dst, int dst_ld,
+                                                 float* __restrict__ dst_sc,
                                                  u32x4* __restrict__ lds, float* __restrict__ scl) {
   constexpr int kM16 = 2 * S::kMT;               // 16-row tiles per wave
   constexpr int kN16 = 2 * S::kNT;               // 16-token tiles per wave
@@ -275,7 +278,23 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     }
   }
   ring_barrier();
-  store_staged<kCols, kWT>(lds, dst, dst_ld, row0, r0, n, c0);
+  if constexpr (GATEUP) {
+    // 16 lanes per token: the group's amax, scale and codes (as quant_groups_kernel computes
+    // them from the stored bf16 act)
+    uint8_t* q = static_cast<uint8_t*>(dst);
+    const int sub = threadIdx.x & 15;
+    for (int r = threadIdx.x >> 4; r < kWT; r += kThreads / 16) {
+      const int p = r0 + r;
+      if (p >= n) break;                                    // uniform over the token's lanes
+      float sc;
+      const u32x2 c = quant_group16(lds[staged_slot<kCols>(r, sub)], sc);
+      const int64_t row = row0 + p;
+      *reinterpret_cast<u32x2*>(q + row * dst_ld + c0 + 8 * sub) = c;
+      if (sub == 0) dst_sc[row * (dst_ld / 128) + c0 / 128] = sc;
+    }
+  } else {
+    store_staged<kCols, kWT>(lds, static_cast<uint16_t*>(dst), dst_ld, row0, r0, n, c0);
+  }
 }
 
 template <bool GATEUP>
@@ -283,17 +302,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
                       const float* __restrict__ src_sc, int src_ld,
                       const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table,
-                      uint16_t* __restrict__ dst, int dst_ld) {
+                      void* __restrict__ dst, int dst_ld, float* __restrict__ dst_sc) {
   __shared__ u32x4 lds[kRingU4];
   __shared__ float scl[kActScales + kWScales];
   const TileItem it = decode_item(table[blockIdx.x]);
   if (it.g < 0) return;
   if (it.narrow)
     tile_product_fp8<GATEUP, Narrow>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
-                                     it.row0, it.wt, dst, dst_ld, lds, scl);
+                                     it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
   else
     tile_product_fp8<GATEUP, Wide>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
-                                   it.row0, it.wt, dst, dst_ld, lds, scl);
+                                   it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
 }
 
 }  // namespace f8t
@@ -305,21 +324,19 @@ bool tiled_fp8_supported(const GroupWeights& gw) {
 
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
-                                    int64_t T, int act_ld, void* act, hipStream_t s) {
-  (void)T;
+                                    int act_ld, void* actq, float* acts, hipStream_t s) {
   f8t::tiled_fp8_kernel<true><<<tiled_grid(gw, max_tiles, true), kThreads, 0, s>>>(
       gw, static_cast<const uint8_t*>(xq), xs, gw.H, perm_tok,
-      tiled_table(gw, tiles, max_tiles, true), static_cast<uint16_t*>(act), act_ld);
+      tiled_table(gw, tiles, max_tiles, true), actq, act_ld, acts);
   return hipGetLastError();
 }
 
 hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const float* acts,
-                                 int act_ld, const int32_t* tiles, int max_tiles, int64_t T,
-                                 void* out, hipStream_t s) {
-  (void)T;
+                                 int act_ld, const int32_t* tiles, int max_tiles, void* out,
+                                 hipStream_t s) {
   f8t::tiled_fp8_kernel<false><<<tiled_grid(gw, max_tiles, false), kThreads, 0, s>>>(
       gw, static_cast<const uint8_t*>(actq), acts, act_ld, nullptr,
-      tiled_table(gw, tiles, max_tiles, false), static_cast<uint16_t*>(out), gw.H);
+      tiled_table(gw, tiles, max_tiles, false), out, gw.H, nullptr);
   return hipGetLastError();
 }
 
