@@ -197,7 +197,7 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     float* acts = at<float>(ws, w, R_ACTS);
     const int64_t rows = T * k + (with_shared ? T : 0);
     LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
-    if (use_tiled(gw, T, k) && tiled_fp8_supported(gw)) {
+    if (use_tiled(gw, T, k) && tiled_fp8_supported(gw, T, rows)) {
       int32_t* tiles = at<int32_t>(ws, w, R_TILES);
       const int max_tiles = tiled_max_tiles(rows, gw.groups);
       LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));

@@ -83,7 +83,8 @@ int tiled_max_tiles(int64_t rows, int groups);  // rows = routed + shared
 // Bytes of a tile list with max_tiles entries and the dispatch tables of both GEMMs.
 int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H);
 bool tiled_supported(const GroupWeights& gw);
-bool tiled_fp8_supported(const GroupWeights& gw);
+// rows = routed + shared rows of the call
+bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows);
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
                               bool shared, int64_t T, int max_tiles, int32_t* tiles,
                               hipStream_t s);

@@ -106,33 +106,35 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   // Ring copies, as in the bf16 kernels: wave copy i fills one 1 KB LDS block of kRowsPerLoad
   // rows; lane l fetches the chunk that the swizzle places at slot l.
   const int lrow = lane / kChunks, lpos = lane % kChunks;
-  const uint8_t* ap[kALoads];
+  // Copy addresses as a wave-uniform base plus a 32-bit lane offset (one VGPR per copy): the
+  // kRowsPerLoad rows of one copy are consecutive rows of one weight matrix.
+  const uint8_t* abase[kALoads];
+  uint32_t aoff[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
-    const int row = (w * kALoads + i) * kRowsPerLoad + lrow;
+    const int row0c = (w * kALoads + i) * kRowsPerLoad;        // the copy's first row
+    const int row = row0c + lrow;
     const int j = lpos ^ ((row >> S::kSwzShift) & (kChunks - 1));
-    const uint8_t* base = wbase;
-    int grow;
     if (GATEUP) {
-      const int half = row / kRW, sub = row % kRW;
-      base = sub < kRW / 2 ? wbase : wup;
-      grow = c0 + half * (kRW / 2) + (sub % (kRW / 2));
+      const int half = row0c / kRW, sub0 = row0c % kRW;
+      abase[i] = sub0 < kRW / 2 ? wbase : wup;
+      aoff[i] = static_cast<uint32_t>((c0 + half * (kRW / 2) + (sub0 % (kRW / 2)) + lrow) * K + 16 * j);
     } else {
-      grow = c0 + row;
+      abase[i] = wbase;
+      aoff[i] = static_cast<uint32_t>((c0 + row) * K + 16 * j);
     }
-    ap[i] = base + static_cast<int64_t>(grow) * K + 16 * j;
   }
   auto src_row = [&](int lt) {         // source row of local token lt (past n: a valid row)
     const int p = min(r0 + lt, n - 1);
     return GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p;
   };
-  const uint8_t* bp[kBLoads];
+  uint32_t boff[kBLoads];
 #pragma unroll
   for (int i = 0; i < kBLoads; ++i) {
     const int lt = (w * kBLoads + i) * kRowsPerLoad + lrow;
     const int row = kWM + lt;
     const int j = lpos ^ ((row >> S::kSwzShift) & (kChunks - 1));
-    bp[i] = src + static_cast<int64_t>(src_row(lt)) * src_ld + 16 * j;
+    boff[i] = static_cast<uint32_t>(src_row(lt)) * static_cast<uint32_t>(src_ld) + 16 * j;
   }
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -164,12 +166,12 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     u32x4* buf = lds + stage * kStageU4;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
-      __builtin_amdgcn_global_load_lds(ap[i] + k0,
+      __builtin_amdgcn_global_load_lds(abase[i] + (aoff[i] + static_cast<uint32_t>(k0)),
                                        (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
                                        16, 0, 0);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
-      __builtin_amdgcn_global_load_lds(bp[i] + k0,
+      __builtin_amdgcn_global_load_lds(src + (boff[i] + static_cast<uint32_t>(k0)),
                                        (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
                                        16, 0, 0);
   };
@@ -203,25 +205,40 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     sp[t] = 0.f;
   }
   fa[0] = read_a(lds, 0);
-
-  auto ktile = [&]<bool NEXT, bool REFILL>(int kt) {
-    const u32x4* cur = lds + (kt % kStages) * kStageU4;
-    // this k-tile's scales: s[h][t] = weight scale h * activation scale of column t, h = 0 for
-    // gate and down tiles, 1 for up tiles
-    float sa[kN16];
-    {
-      const float* a = scl + kt * kWT + wn * (16 * kN16) + r16 * kN16;
+  // Scales of k-tile kt: sc[h][t] = weight scale h * activation scale of column t, h = 0 for
+  // gate and down tiles, 1 for up tiles. The next k-tile's are read halfway through a k-tile.
+  float sa[kN16], w0, w1;
+  auto read_scales = [&](int kt) {
+    const float* a = scl + kt * kWT + wn * (16 * kN16) + r16 * kN16;
 #pragma unroll
-      for (int t = 0; t < kN16; ++t) sa[t] = a[t];
-    }
-    const float w0 = wsc[(GATEUP ? 0 : wm) * nk + kt];
-    const float w1 = GATEUP ? wsc[nk + kt] : w0;
-    float s[2][kN16];
+    for (int t = 0; t < kN16; ++t) sa[t] = a[t];
+    w0 = wsc[(GATEUP ? 0 : wm) * nk + kt];
+    w1 = GATEUP ? wsc[nk + kt] : w0;
+  };
+  float sc[2][kN16];
+  auto make_scales = [&]() {
 #pragma unroll
     for (int t = 0; t < kN16; ++t) {
-      s[0][t] = w0 * sa[t];
-      s[1][t] = w1 * sa[t];
+      sc[0][t] = w0 * sa[t];
+      sc[1][t] = w1 * sa[t];
     }
+  };
+  read_scales(0);
+  make_scales();
+
+  // One step: the pending products are scaled and added just before the MFMA that replaces
+  // them, one tile column at a time (VALU 4, MFMA 1), with the next A fragment's two reads
+  // after the first MFMA.
+  auto sched_step = [&]() {
+#pragma unroll
+    for (int t = 0; t < kN16; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (t == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  auto ktile = [&]<bool NEXT, bool REFILL>(int kt) {
+    const u32x4* cur = lds + (kt % kStages) * kStageU4;
 #pragma unroll
     for (int i = 0; i < kM16; ++i) {
       const bool last = i == kM16 - 1;
@@ -229,6 +246,7 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
       // last step, or zeros with zero scales before the first k-tile)
       const int pi = i == 0 ? kM16 - 1 : i - 1;
       const int h = GATEUP && i >= kM16 / 2 ? 1 : 0;
+      if (NEXT && i == kM16 / 2) read_scales(kt + 1);
       if (!last) fa[(i + 1) & 1] = read_a(cur, i + 1);
       if (last && NEXT) {
         // every earlier MFMA stays above the barrier
@@ -242,12 +260,25 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
         acc[pi][t] += p[t] * sp[t];
         p[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             fa[i & 1], fb[t], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
-        sp[t] = s[h][t];
+        sp[t] = sc[h][t];
         if (last && NEXT) fb[t] = read_b(nxt, t);
       }
       if (last && NEXT) {
         fa[0] = read_a(nxt, 0);
         if constexpr (REFILL) issue(kt % kStages, (kt + kStages) * 128);
+        make_scales();
+        // next k-tile's B fragments one tile column at a time behind this step's MFMAs, then
+        // its first A fragment and the refill copies
+#pragma unroll
+        for (int t = 0; t < kN16; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if constexpr (REFILL) __builtin_amdgcn_sched_group_barrier(0x020, kLoads, 0);
+      } else {
+        sched_step();
       }
     }
   };
@@ -317,9 +348,14 @@ void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
 
 }  // namespace f8t
 
-bool tiled_fp8_supported(const GroupWeights& gw) {
+bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows) {
+  // the copies address operands with 32-bit byte offsets from a weight matrix, xq or actq
+  const int64_t Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  constexpr int64_t kMaxOffset = int64_t{1} << 32;
   return tiled_supported(gw) && gw.H / 128 <= f8t::kMaxKBlocks &&
-         gw.I / 128 <= f8t::kMaxKBlocks && gw.Is / 128 <= f8t::kMaxKBlocks;
+         gw.I / 128 <= f8t::kMaxKBlocks && gw.Is / 128 <= f8t::kMaxKBlocks &&
+         T * gw.H < kMaxOffset && rows * Imax < kMaxOffset &&
+         2 * Imax * gw.H < kMaxOffset;
 }
 
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
