@@ -51,12 +51,13 @@ namespace lbmoe {
 // wide: 2 x 4 waves of 128 x 64 (256 tokens); narrow: 2 x 4 waves of 128 x 32 (128 tokens)
 using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
 using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
-// router logits: 4 x 2 waves of 64 x 32 (64 tokens), so that T = 8192 gives 128 workgroups
+// router logits: 4 x 2 waves of 64 x 32 (256 experts x 64 tokens); for at most 128 experts
+// 4 x 2 waves of 32 x 32 (128 x 64) with a ring small enough for two workgroups per CU
 using RouterShape = TileShape<4, 2, 1, 64, 3>;
+using RouterShape128 = TileShape<4, 1, 1, 64, 3>;
 constexpr int kLdsU4 = Wide::kStages * Wide::kStageU4 > Narrow::kStages * Narrow::kStageU4
                            ? Wide::kStages * Wide::kStageU4
                            : Narrow::kStages * Narrow::kStageU4;
-static_assert(RouterShape::kStages * RouterShape::kStageU4 <= kLdsU4, "router ring too large");
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
 
 // ---- tile list -------------------------------------------------------------------------------
@@ -220,7 +221,7 @@ enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 // Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
 // expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
 // src (down) / dst.
-template <int MODE, class S>
+template <int MODE, class S, int kLdsCap = kLdsU4>
 __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint16_t* __restrict__ src,
                                              int src_ld, const int32_t* __restrict__ perm_tok,
                                              int g, int r0, int n, int row0, int wt,
@@ -232,11 +233,14 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   constexpr int kRowsPerLoad = S::kRowsPerLoad, kALoads = S::kALoads, kBLoads = S::kBLoads;
   constexpr int kLoads = S::kLoads, kKSteps = S::kKSteps, kStageU4 = S::kStageU4;
   constexpr int kSwzShift = S::kSwzShift;
+  constexpr int kRows = S::kRows;                  // weight rows of the tile
+  static_assert(ROUTER || kRows == kWM, "expert GEMMs take kWM weight rows per tile");
+  static_assert(!GATEUP || kMT % 2 == 0, "gate_up pairs a wave's gate tiles with its up tiles");
   const bool shared = !ROUTER && g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int H = gw.H;
   const int K = (GATEUP || ROUTER) ? H : Ig;
-  const int c0 = wt * (GATEUP ? kWM / 2 : kWM);      // first channel / output column
+  const int c0 = wt * (GATEUP ? kRows / 2 : kRows);  // first channel / output column
 
   const int lane = threadIdx.x & 63;
   // Wave index as a scalar: LDS destinations of the copies (M0) are then computed on the SALU.
@@ -286,7 +290,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 #pragma unroll
   for (int i = 0; i < kBLoads; ++i) {
     const int lt = (w * kBLoads + i) * kRowsPerLoad + lrow;     // local token
-    const int row = kWM + lt;
+    const int row = kRows + lt;
     const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
     const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
     const int srow = ROUTER ? p : (GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p);
@@ -312,7 +316,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
       __builtin_amdgcn_global_load_lds(bp[i] + k0,
-                                       (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
+                                       (lds_ptr)(buf + (kRows + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
                                        16, 0, 0);
   };
 
@@ -332,7 +336,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 #pragma unroll
     for (int i = 0; i < kMT; ++i) fa[i] = cur[S::swz(wm * kRW + 32 * i + mr, j)];
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) fb[t] = cur[S::swz(kWM + wn * (kNT * 32) + 32 * t + mr, j)];
+    for (int t = 0; t < kNT; ++t) fb[t] = cur[S::swz(kRows + wn * (kNT * 32) + 32 * t + mr, j)];
   };
   auto mfma_all = [&](const u32x4 (&fa)[kMT], const u32x4 (&fb)[kNT]) {
 #pragma unroll
@@ -405,7 +409,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     // (kCols * 2 contiguous bytes per token) with 16-byte lanes. Storing straight from the
     // accumulators would write 16-byte pieces of 32 token rows per instruction.
     constexpr int kCols = GATEUP ? kWM / 2 : kWM;            // output columns per tile
-    static_assert(S::kWT * (kCols / 8) <= kLdsU4, "staged tile exceeds the LDS ring");
+    static_assert(S::kWT * (kCols / 8) <= kLdsCap, "staged tile exceeds the LDS ring");
     ring_barrier();                                           // every wave is done with the ring
     char* st = reinterpret_cast<char*>(lds);
 #pragma unroll
@@ -454,16 +458,18 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 }
 
 // ---- the kernels -----------------------------------------------------------------------------
-// Router logits: one workgroup per (token tile of RouterShape::kWT, weight tile), no tile list.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// Router logits: one workgroup per (token tile of S::kWT, weight tile of S::kRows experts), no
+// tile list.
+template <class S>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
 void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T, int n_wtiles,
                          uint16_t* __restrict__ logits) {
-  __shared__ u32x4 lds[kLdsU4];
-  const int logical = xcd_item(blockIdx.x, (T + RouterShape::kWT - 1) / RouterShape::kWT * n_wtiles);
+  __shared__ u32x4 lds[S::kStages * S::kStageU4];
+  const int logical = xcd_item(blockIdx.x, (T + S::kWT - 1) / S::kWT * n_wtiles);
   if (logical < 0) return;
   const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  tile_product<kRouter, RouterShape>(gw, x, gw.H, nullptr, 0, ti * RouterShape::kWT, T, 0, wt,
-                                     logits, gw.E, lds);
+  tile_product<kRouter, S, S::kStages * S::kStageU4>(gw, x, gw.H, nullptr, 0, ti * S::kWT, T, 0,
+                                                     wt, logits, gw.E, lds);
 }
 
 template <int MODE>
@@ -553,18 +559,25 @@ hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld
 
 bool tiled_router_supported(int E, int H) { return H % RouterShape::kBK == 0 && E >= 1; }
 
+template <class S>
+static hipError_t launch_router_shape(const GroupWeights& gw, const void* x, int64_t T, void* logits,
+                                      hipStream_t s) {
+  const int n_wtiles = (gw.E + S::kRows - 1) / S::kRows;
+  const int64_t n_ttiles = (T + S::kWT - 1) / S::kWT;
+  router_tiled_kernel<S><<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
+      gw, static_cast<const uint16_t*>(x), static_cast<int>(T), n_wtiles,
+      static_cast<uint16_t*>(logits));
+  return hipGetLastError();
+}
+
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s) {
   GroupWeights gw{};
   gw.gate_up = wg;
   gw.E = E;
   gw.H = H;
-  const int n_wtiles = (E + kWM - 1) / kWM;
-  const int64_t n_ttiles = (T + RouterShape::kWT - 1) / RouterShape::kWT;
-  router_tiled_kernel<<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(x), static_cast<int>(T), n_wtiles,
-      static_cast<uint16_t*>(logits));
-  return hipGetLastError();
+  if (E <= RouterShape128::kRows) return launch_router_shape<RouterShape128>(gw, x, T, logits, s);
+  return launch_router_shape<RouterShape>(gw, x, T, logits, s);
 }
 
 }  // namespace lbmoe

@@ -18,9 +18,11 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kWM = 256;                            // weight rows per workgroup
 
 // One token-tile shape: WAVES_M x (kWaves / WAVES_M) waves, each owning MT x NT units of 32
-// weight rows x 32 tokens, k-tiles of BK bf16 (2 * BK bytes per row), STAGES LDS buffers.
+// weight rows x 32 tokens, k-tiles of BK bf16 (2 * BK bytes per row), STAGES LDS buffers. The
+// expert GEMMs use kRows = kWM weight rows; the router may use fewer.
 template <int WAVES_M, int MT, int NT, int BK, int STAGES>
 struct TileShape {
+  static constexpr int kRows = WAVES_M * MT * 32;             // weight rows per workgroup
   static constexpr int kWavesM = WAVES_M;
   static constexpr int kWavesN = kWaves / WAVES_M;
   static constexpr int kMT = MT;
@@ -31,20 +33,18 @@ struct TileShape {
   static constexpr int kStages = STAGES;
   static constexpr int kChunks = BK / 8;                      // 16-byte chunks per LDS row
   static constexpr int kRowsPerLoad = 64 / kChunks;           // rows one wave copy covers
-  static constexpr int kALoads = kWM / kRowsPerLoad / kWaves;  // wave copies per stage (weights)
+  static constexpr int kALoads = kRows / kRowsPerLoad / kWaves;  // wave copies per stage (weights)
   static constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;  // wave copies per stage (tokens)
   static constexpr int kLoads = kALoads + kBLoads;
-  static constexpr int kStageU4 = (kWM + kWT) * kChunks;      // 16-byte slots per stage
+  static constexpr int kStageU4 = (kRows + kWT) * kChunks;    // 16-byte slots per stage
   static constexpr int kKSteps = BK / 16;                     // bf16 MFMA k-steps per k-tile
   // Chunk j of row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
   // kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
   static constexpr int kSwzShift = kChunks == 4 ? 2 : 1;
-  static_assert(WAVES_M * MT * 32 == kWM, "waves must tile the weight rows");
   static_assert(kChunks == 4 || kChunks == 8, "BK must be 32 or 64");
-  static_assert(kALoads * kRowsPerLoad * kWaves == kWM && kBLoads * kRowsPerLoad * kWaves == kWT,
+  static_assert(kALoads * kRowsPerLoad * kWaves == kRows && kBLoads * kRowsPerLoad * kWaves == kWT,
                 "copies must tile the stage");
   static_assert(kKSteps % 2 == 0, "the next k-tile's first fragments go to register buffer 0");
-  static_assert(MT % 2 == 0, "gate_up pairs a wave's gate tiles with its up tiles");
   static __device__ __forceinline__ int swz(int r, int j) {
     return r * kChunks + (j ^ ((r >> kSwzShift) & (kChunks - 1)));
   }
