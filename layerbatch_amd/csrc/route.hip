@@ -9,10 +9,13 @@
 // The shared-expert gate sigmoid(x . w_sg) follows qwen3_5.py:897, :903 with the dot product
 // rounded to bf16 as F.linear's bf16 output is.
 //
-// One wave per token; lane l holds experts l, l+64, ... in registers. Selection is a radix
-// select on order-preserving 32-bit keys of z: 32 ballot rounds find the k-th largest key
-// (no cross-lane shuffles), equal keys at the threshold are taken in ascending expert index,
-// and the k winners are ranked against each other through LDS.
+// One wave per token; lane l holds experts l, l+64, ... in registers as order-preserving
+// 32-bit keys of z. Selection is k rounds of argmax: each lane keeps its best remaining key
+// (ties to the lower expert), the wave maximum comes from a DPP reduction within 16-lane rows
+// and four lane reads, and the winner is the lane holding that key (on a tie between lanes,
+// the lowest expert index). Round r's winner is slot r, so the slots come out in the required
+// order, and the winner's key is removed. Most of the work is vector ALU; the scalar unit,
+// which a CU's waves share, only combines the four row maxima.
 #include <float.h>
 
 #include "common.hpp"
@@ -26,7 +29,25 @@ __device__ __forceinline__ uint32_t order_key(float z) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-constexpr int kMaxK = 32;
+// Wave-wide maximum of v (DPP within each 16-lane row, then the four row maxima).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xf, 0xf, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xf, 0xf, false)));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false));
+  const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return min(min(r0, r1), min(r2, r3));
+}
 
 template <int EPL>
 __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ logits,
@@ -36,8 +57,6 @@ __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ l
                                                   int E, int H, int k, void* idx_out,
                                                   int idx_bytes, uint16_t* __restrict__ topw,
                                                   float* __restrict__ sgate) {
-  __shared__ uint32_t sel_key[4][kMaxK];
-  __shared__ int sel_e[4][kMaxK];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
@@ -66,53 +85,44 @@ __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ l
     if (j * kWave + lane < E) part += expf(z[j] - m);
   const float S = wave_sum(part);
 
-  // Largest threshold with at least k keys >= threshold, built bit by bit from the top.
-  uint32_t thr = 0;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = thr | (1u << b);
-    int cnt = 0;
+  // k rounds of argmax; lane r < k keeps round r's winner (expert and key)
+  int my_e = 0;
+  uint32_t my_key = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t best = key[0];
+    int bj = 0;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-    if (cnt >= k) thr = cand;
-  }
-  int above = 0;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) above += __popcll(__ballot(key[j] > thr));
-  // Winners: every key above thr, then keys equal to thr in ascending expert index.
-  int n_sel = 0, eq_seen = 0;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const uint64_t eq = __ballot(key[j] == thr);
-    const bool is_eq = key[j] == thr;
-    const bool take = key[j] > thr || (is_eq && eq_seen + mask_rank(eq) < k - above);
-    const uint64_t tk = __ballot(take);
-    if (take) {
-      const int pos = n_sel + mask_rank(tk);
-      sel_key[wave][pos] = key[j];
-      sel_e[wave][pos] = j * kWave + lane;
+    for (int j = 1; j < EPL; ++j)
+      if (key[j] > best) {
+        best = key[j];
+        bj = j;
+      }
+    const uint32_t wmax = wave_max_u32(best);
+    const uint64_t holders = __ballot(best == wmax);
+    int win;                                            // winning expert
+    if (__popcll(holders) == 1) {
+      const int wl = __builtin_ctzll(holders);
+      win = __builtin_amdgcn_readlane(bj * kWave + lane, wl);
+    } else {
+      win = wave_min_i32(best == wmax ? bj * kWave + lane : 0x7fffffff);
     }
-    n_sel += __popcll(tk);
-    eq_seen += __popcll(eq);
+    const int wj = win / kWave, wl = win % kWave;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      if (j == wj && lane == wl) key[j] = 0u;
+    if (lane == r) {
+      my_e = win;
+      my_key = wmax;
+    }
   }
-  // sel_* rows are private to this wave, whose LDS accesses complete in program order.
-  __builtin_amdgcn_wave_barrier();
-  // Lane s < k owns winner s; its output slot is the number of winners ordered before it.
   float p = 0.f;
-  int my_e = 0, slot = 0;
   if (lane < k) {
-    const uint32_t mk = sel_key[wave][lane];
-    my_e = sel_e[wave][lane];
-    for (int i = 0; i < k; ++i) {
-      const uint32_t ok = sel_key[wave][i];
-      const int oe = sel_e[wave][i];
-      slot += (ok > mk || (ok == mk && oe < my_e)) ? 1 : 0;
-    }
-    const uint32_t u = (mk & 0x80000000u) ? (mk & 0x7fffffffu) : ~mk;   // key -> z
+    const uint32_t u = (my_key & 0x80000000u) ? (my_key & 0x7fffffffu) : ~my_key;   // key -> z
     p = expf(__uint_as_float(u) - m) / S;
   }
   const float psum = wave_sum(p);
   if (lane < k) {
-    const int64_t o = static_cast<int64_t>(t) * k + slot;
+    const int64_t o = static_cast<int64_t>(t) * k + lane;
     topw[o] = static_cast<uint16_t>(f2bf(p / psum));
     if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o] = my_e;
     else reinterpret_cast<int32_t*>(idx_out)[o] = my_e;

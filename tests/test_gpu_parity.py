@@ -207,3 +207,34 @@ def test_cpu_tensor_raises(gpu):
     blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
     with pytest.raises(RuntimeError):
         blk(torch.zeros((4, 1024), dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("T,E,k,levels,bias", [(300, 128, 8, 3, False), (257, 512, 10, 4, False),
+                                               (64, 1000, 32, 2, True), (100, 64, 32, 5, False),
+                                               (77, 200, 7, 1, True), (129, 16, 2, 2, False)])
+def test_route_ties(gpu, T, E, k, levels, bias):
+    """Selection on logits with only a few distinct values, so that most selections are decided
+    by the tie rule (lower expert index first), within and across lanes; with -inf and NaN
+    logits and an optional bias that itself has ties."""
+    from layerbatch_amd._lib import LbmoeLayer
+    rng = np.random.default_rng(T * 7 + E)
+    z = rng.integers(0, levels, size=(T, E)).astype(np.float32) * 0.5 - 1.0
+    z[0, :-1] = -np.inf                     # one finite logit, the rest tie at -inf
+    z[1, ::3] = np.nan                      # NaN logits are never preferred
+    zb = torch.tensor(z).to(torch.bfloat16)
+    L = LbmoeLayer()
+    L.hidden_size, L.num_experts, L.top_k, L.moe_intermediate_size = 128, E, k, 128
+    b_np = None
+    if bias:
+        b_np = (rng.integers(0, 2, size=E) * 0.25).astype(np.float32)
+        b = torch.tensor(b_np, device=gpu)
+        L.logit_bias = b.data_ptr()
+    logits = zb.to(gpu)
+    idx = torch.empty((T, k), dtype=torch.int32, device=gpu)
+    w = torch.empty((T, k), dtype=torch.bfloat16, device=gpu)
+    _lib.check(_lib.lib().lbmoe_route(ctypes.byref(L), _lib.ptr(logits), None, T, _lib.ptr(idx), 4,
+                                      _lib.ptr(w), None, _lib.stream_of(gpu)), "lbmoe_route")
+    torch.cuda.synchronize()
+    ln = to_np(zb)
+    ln = np.where(np.isnan(ln), -np.inf, ln)   # the oracle's view of a NaN logit
+    gc.check_route(to_np(idx), bf16_bits_of(w), ln, b_np, k)
