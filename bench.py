@@ -2,7 +2,7 @@
 """Benchmark of the MoE feed-forward layer on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--T 128] [--prefill-T 8192] [--no-cpu-baseline]
-                    [--no-prefill] [--no-extra] [--copy-probe-mib N]
+                    [--no-prefill] [--no-extra] [--copy-probe-mib N] [--only-extra TEXT]
 
 Headline workload: the Qwen3-30B-A3B MoE layer (H=2048, E=128, top-8, I=768, bf16 weights
 ~N(0,0.02), activations ~N(0,1), synthetic, seed 0) at decode T=128. One step is one call of
@@ -49,6 +49,10 @@ def parse():
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
     p.add_argument("--no-extra", action="store_true",
                    help="skip the other configurations (decode sweep, E=512 layer, fp8 variant)")
+    p.add_argument("--only-extra", default=None, metavar="TEXT",
+                   help="run only the extra configurations whose name contains TEXT (for example "
+                        "'fp8-e4m3 prefill') and print them as one JSON line, without the "
+                        "headline measurement")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="also run a plain copy kernel (torch.neg, fp32) over this many MiB, "
                         "3 times: the calibration dispatch for FETCH_SIZE/WRITE_SIZE counters")
@@ -239,10 +243,11 @@ def measure_wall(blks, x, steps, warmup):
     return us, int((counts > 0).sum())
 
 
-def extra_configs(dev, steps):
+def extra_configs(dev, steps, only=None):
     """The other configurations of the measurement plan, each at one GPU: the decode sweep of
     the headline layer, the Qwen3-Next-style E=512 layer with a shared expert, and its fp8
-    variant. Every entry: back-to-back us per call and the algorithmic rate."""
+    variant. Every entry: back-to-back us per call and the algorithmic rate. only: run just
+    the configurations whose name contains this text."""
     import torch
     from layerbatch_amd.synth import SHAPES, make_x
     out = []
@@ -257,32 +262,45 @@ def extra_configs(dev, steps):
                 "TFLOPs": round(tf, 2), "frac_of_mfma_peak": round(tf / peak_tf, 4),
                 "bound": bound}
 
+    def wanted(name):
+        return only is None or only in name
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
     # decode sweep of the headline layer; four weight copies rotate when a call touches few
     # experts, so the weights do not stay in the 256 MB MALL between calls
     shape = SHAPES["qwen3-30b-a3b"]
-    blk, _ = layer_inputs(shape, 1, 0, False, dev)
-    copies = [blk] + [layer_inputs(shape, 1, 1 + i, False, dev)[0] for i in range(3)]
-    g = torch.Generator(device=dev)
-    g.manual_seed(7)
-    for T in (1, 16, 64, 256):
+    sweep = [(T, "qwen3-30b-a3b decode" + (" (4 weight copies rotating)" if T <= 16 else ""))
+             for T in (1, 16, 64, 256)]
+    # the activations are drawn for every configuration, so that each one sees the same inputs
+    # whichever are selected
+    copies = None
+    if any(wanted(name) for _, name in sweep):
+        copies = [layer_inputs(shape, 1, i, False, dev)[0] for i in range(4)]
+    for T, name in sweep:
         x = make_x(g, T, shape.hidden_size, device=dev)
-        blks = copies if T <= 16 else copies[:1]
-        us, hit = measure_wall(blks, x, steps, max(2, steps // 5))
-        out.append(entry("qwen3-30b-a3b decode" + (" (4 weight copies rotating)" if T <= 16 else ""),
-                         shape, T, us, hit, 2, "hbm"))
-    del blk, copies
+        if wanted(name):
+            blks = copies if T <= 16 else copies[:1]
+            us, hit = measure_wall(blks, x, steps, max(2, steps // 5))
+            out.append(entry(name, shape, T, us, hit, 2, "hbm"))
+        del x
+    del copies
     torch.cuda.empty_cache()
 
     shape = SHAPES["qwen3-next-e512"]
     for fp8 in (False, True):
-        blk, _ = layer_inputs(shape, 1, 0, False, dev, fp8=fp8)
-        for T in ((128, 16384) if fp8 else (128, 4096)):
+        runs = [(T, "qwen3-next-e512" + (" fp8-e4m3" if fp8 else "") +
+                 (" prefill" if T > 256 else " decode"))
+                for T in ((128, 16384) if fp8 else (128, 4096))]
+        blk = (layer_inputs(shape, 1, 0, False, dev, fp8=fp8)[0]
+               if any(wanted(name) for _, name in runs) else None)
+        for T, name in runs:
             x = make_x(g, T, shape.hidden_size, device=dev)
-            n = steps if T <= 256 else max(3, steps // 5)
-            us, hit = measure_wall([blk], x, n, max(1, n // 5))
-            out.append(entry("qwen3-next-e512" + (" fp8-e4m3" if fp8 else "") +
-                             (" prefill" if T > 256 else " decode"), shape, T, us, hit,
-                             1 if fp8 else 2, "mfma" if fp8 and T > 256 else "hbm"))
+            if wanted(name):
+                n = steps if T <= 256 else max(3, steps // 5)
+                us, hit = measure_wall([blk], x, n, max(1, n // 5))
+                out.append(entry(name, shape, T, us, hit, 1 if fp8 else 2,
+                                 "mfma" if fp8 and T > 256 else "hbm"))
             del x
         del blk
         torch.cuda.empty_cache()
@@ -298,6 +316,9 @@ def main():
     import torch
     from layerbatch_amd.synth import SHAPES
     dev = torch.device("cuda:0")
+    if args.only_extra is not None:
+        print(json.dumps({"metric": METRIC, "extra": extra_configs(dev, args.steps, args.only_extra)}))
+        return
     hip = HipEvents()
     shape = SHAPES[args.shape]
 
