@@ -275,13 +275,50 @@ class Qwen3_5SparseMoeBlock(nn.Module):
     def quantize_fp8_(self):
         """Convert expert (and shared-expert) weights to e4m3fn + 128x128 block scales."""
         ex = self.experts
-        ex.gate_up_q, ex.gate_up_scale = _quantize_blocks(ex.gate_up_proj)
-        ex.down_q, ex.down_scale = _quantize_blocks(ex.down_proj)
-        ex.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+        experts = _quantize_blocks(ex.gate_up_proj) + _quantize_blocks(ex.down_proj)
+        shared = None
         if self.shared_expert is not None:
             se = self.shared_expert
-            se.q = {"gate": _quantize_blocks(se.gate_proj.weight),
-                    "up": _quantize_blocks(se.up_proj.weight),
-                    "down": _quantize_blocks(se.down_proj.weight)}
+            shared = {"gate": _quantize_blocks(se.gate_proj.weight),
+                      "up": _quantize_blocks(se.up_proj.weight),
+                      "down": _quantize_blocks(se.down_proj.weight)}
+        return self.load_fp8_(experts, shared)
+
+    @torch.no_grad()
+    def load_fp8_(self, experts, shared=None):
+        """Install e4m3fn weights with 128x128 block scales, e.g. from an fp8 checkpoint.
+
+        experts: (gate_up codes [E,2I,H], gate_up scales [E,2I/128,H/128], down codes [E,H,I],
+        down scales [E,H/128,I/128]); shared: {"gate"|"up"|"down": (codes, scales)} with the
+        shared expert's [Is,H], [Is,H], [H,Is] shapes. Codes are uint8 (or float8_e4m3fn)
+        tensors on the block's device, scales fp32.
+        """
+        ex = self.experts
+        E, H, I = ex.num_experts, ex.hidden_size, ex.intermediate_size
+
+        def codes_scales(q, s, shape, name):
+            if q.dtype == torch.float8_e4m3fn:
+                q = q.view(torch.uint8)
+            if q.dtype != torch.uint8 or tuple(q.shape) != tuple(shape):
+                raise RuntimeError(f"{name}: expected uint8 codes of shape {tuple(shape)}, got "
+                                   f"{q.dtype} {tuple(q.shape)}")
+            sshape = (*shape[:-2], shape[-2] // 128, shape[-1] // 128)
+            if s.dtype != torch.float32 or tuple(s.shape) != sshape:
+                raise RuntimeError(f"{name} scales: expected float32 {sshape}, got "
+                                   f"{s.dtype} {tuple(s.shape)}")
+            return q.contiguous(), s.contiguous()
+
+        gu_q, gu_s, d_q, d_s = experts
+        ex.gate_up_q, ex.gate_up_scale = codes_scales(gu_q, gu_s, (E, 2 * I, H), "experts.gate_up_proj")
+        ex.down_q, ex.down_scale = codes_scales(d_q, d_s, (E, H, I), "experts.down_proj")
+        ex.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+        if self.shared_expert is not None:
+            if shared is None:
+                raise RuntimeError("this block has a shared expert: its fp8 weights are required")
+            se = self.shared_expert
+            Is = se.gate_proj.weight.shape[0]
+            shapes = {"gate": (Is, H), "up": (Is, H), "down": (H, Is)}
+            se.q = {n: codes_scales(*shared[n], shapes[n], f"shared_expert.{n}_proj.weight")
+                    for n in ("gate", "up", "down")}
             se.weight_dtype = _lib.LBMOE_W_FP8_E4M3
         return self

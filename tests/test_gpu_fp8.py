@@ -1,11 +1,13 @@
 """GPU parity of the fp8 (OCP e4m3fn) variant against the CPU oracle's dequantised fp32 path."""
 import ctypes
+import os
 
 import numpy as np
 import pytest
 import torch
 
 from layerbatch_amd import _lib
+from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
 from layerbatch_amd.synth import MoEShape, make_layer, make_x
 from oracle import moe as om
 from tests import gpu_checks as gc
@@ -112,3 +114,28 @@ def test_fp8_rejects_unsupported_width(gpu, lbmoe):
     L.moe_intermediate_size, L.weight_dtype = 384, _lib.LBMOE_W_FP8_E4M3
     n = ctypes.c_size_t(0)
     assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), 4, ctypes.byref(n)) == -2
+
+
+@pytest.mark.parametrize("T", [64, 600])      # streaming and LDS-tiled fp8 GEMMs
+def test_fp8_checkpoint_matches_quantize(gpu, tmp_path, T):
+    """An fp8 checkpoint written by the offline converter (CPU quantisation) and loaded into a
+    block gives bit-identical outputs to quantize_fp8_ (GPU quantisation) of the same weights."""
+    from safetensors.torch import save_file
+    from layerbatch_amd import checkpoint as ck
+    shape = MoEShape(1024, 16, 2, 512, 256)
+    w, g = make_layer(shape, seed=12)
+    x = make_x(g, T, shape.hidden_size).to(gpu)
+    p = "model." + ck.mlp_prefix(0)
+    names = {"gate": "gate.weight", "gate_up": "experts.gate_up_proj", "down": "experts.down_proj",
+             "sh_gate": "shared_expert.gate_proj.weight", "sh_up": "shared_expert.up_proj.weight",
+             "sh_down": "shared_expert.down_proj.weight", "sh_gate_w": "shared_expert_gate.weight"}
+    src, dst = tmp_path / "bf16", tmp_path / "fp8"
+    os.makedirs(src)
+    save_file({p + n: w[k].contiguous() for k, n in names.items()}, str(src / "model.safetensors"))
+    assert ck.quantize_checkpoint_fp8(str(src), str(dst)) == 5
+    loaded = Qwen3_5SparseMoeBlock(1024, 16, 2, 512, 256).to(device=gpu, dtype=torch.bfloat16)
+    ck.load_moe_block(loaded, str(dst), 0)
+    ref = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu).quantize_fp8_()
+    y1, y2 = loaded(x), ref(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)

@@ -12,16 +12,19 @@ pytestmark = pytest.mark.gpu
 SHAPE = MoEShape(1024, 16, 2, 512, 256)
 
 
-def _setup(gpu, T, seed=3):
+def _setup(gpu, T, seed=3, fp8=False):
     w, g = make_layer(SHAPE, seed=seed)
     blk = _block(SHAPE, {k: v.to(gpu) for k, v in w.items()}, gpu)
+    if fp8:
+        blk.quantize_fp8_()
     xs = [make_x(g, T, SHAPE.hidden_size).to(gpu) for _ in range(3)]
     return blk, xs
 
 
-@pytest.mark.parametrize("T", [40, 512])     # streaming GEMMs, LDS-tiled GEMMs
-def test_graph_replay_matches_eager(gpu, T):
-    blk, xs = _setup(gpu, T)
+# streaming GEMMs, LDS-tiled GEMMs; bf16 and fp8 weights
+@pytest.mark.parametrize("T,fp8", [(40, False), (512, False), (40, True), (512, True)])
+def test_graph_replay_matches_eager(gpu, T, fp8):
+    blk, xs = _setup(gpu, T, fp8=fp8)
     ws_e = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=gpu)
     ws_g = torch.empty_like(ws_e)
     static_x = xs[0].clone()
