@@ -68,3 +68,35 @@ def test_repeated_calls_are_deterministic(gpu):
     ys = [blk(xs[1]) for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
+
+
+def test_decode_bucket_graphs(gpu):
+    """The engine's decode capture (model_runner.py:1463-1507): one graph per batch bucket,
+    captured from the largest bucket down in a shared memory pool, all reading slices of one
+    static input buffer whose rows past the live batch are zeros (padded rows are routed like
+    real ones). Every bucket's replay matches an eager call on the same slice bit for bit."""
+    buckets = [1, 2, 4, 8, 16, 32, 48, 64]
+    w, g = make_layer(SHAPE, seed=11)
+    blk = _block(SHAPE, {k: v.to(gpu) for k, v in w.items()}, gpu)
+    static_x = torch.zeros((max(buckets), SHAPE.hidden_size), dtype=torch.bfloat16, device=gpu)
+    outputs = torch.zeros_like(static_x)
+    graphs, pool = {}, None
+    for bs in reversed(buckets):
+        outputs[:bs] = blk(static_x[:bs])                        # warm-up
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool):
+            outputs[:bs] = blk(static_x[:bs])
+        if pool is None:
+            pool = graph.pool()
+        graphs[bs] = graph
+        torch.cuda.synchronize()
+    for bs in buckets:
+        live = max(1, bs - 1 - bs // 4)                          # a partly filled bucket
+        x = make_x(g, live, SHAPE.hidden_size).to(gpu)
+        static_x.zero_()
+        static_x[:live] = x
+        graphs[bs].replay()
+        torch.cuda.synchronize()
+        y_e = blk(static_x[:bs].clone())
+        torch.cuda.synchronize()
+        assert torch.equal(outputs[:bs], y_e), f"bucket {bs} replay differs from the eager result"
