@@ -243,6 +243,51 @@ def measure_wall(blks, x, steps, warmup):
     return us, int((counts > 0).sum())
 
 
+def norm_config(name, shape, hid, res, nw, steps, dev, eps=1e-6):
+    """Back-to-back µs per call of the block with the decoder layer's residual add + RMSNorm:
+    fused (lbmoe_forward_norm), the block alone on an already normalised input, and the
+    reference's torch statements for the add and the norm followed by the block."""
+    import torch
+    from layerbatch_amd import _lib
+    T = hid.shape[0]
+    blk, _ = layer_inputs(shape, 1, 0, False, dev)
+    L = blk.layer()
+    lib = _lib.lib()
+    stream = _lib.stream_of(dev)
+    ws = torch.empty(_lib.workspace_size(L, T), dtype=torch.uint8, device=dev)
+    y = torch.empty_like(hid)
+    new_res = torch.empty_like(res)
+    xn = torch.empty_like(hid)
+    fused = (ctypes.byref(L), _lib.ptr(hid), _lib.ptr(res), _lib.ptr(nw), eps, T, _lib.ptr(y),
+             _lib.ptr(new_res), _lib.ptr(ws), ws.numel(), stream)
+    plain = (ctypes.byref(L), _lib.ptr(xn), T, _lib.ptr(y), _lib.ptr(ws), ws.numel(), stream)
+
+    def torch_norm():
+        h = res + hid                                     # qwen3_5.py:998
+        o = h.float()                                     # Qwen3_5RMSNorm, :48-55
+        o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + eps)
+        xn.copy_((o * (1.0 + nw.float())).type_as(h))
+
+    def timed(fn):
+        for _ in range(max(2, steps // 5)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps * 1e6
+
+    torch_norm()
+    us_fused = timed(lambda: _lib.check(lib.lbmoe_forward_norm(*fused), "lbmoe_forward_norm"))
+    us_plain = timed(lambda: _lib.check(lib.lbmoe_forward(*plain), "lbmoe_forward"))
+    us_torch = timed(lambda: (torch_norm(), lib.lbmoe_forward(*plain)))
+    del blk
+    return {"config": name, "T": T, "us_per_call_fused": round(us_fused, 1),
+            "us_per_call_block_only": round(us_plain, 1),
+            "us_per_call_torch_norm_then_block": round(us_torch, 1), "bound": "hbm"}
+
+
 def extra_configs(dev, steps, only=None):
     """The other configurations of the measurement plan, each at one GPU: the decode sweep of
     the headline layer, the Qwen3-Next-style E=512 layer with a shared expert, and its fp8
@@ -286,6 +331,17 @@ def extra_configs(dev, steps, only=None):
         del x
     del copies
     torch.cuda.empty_cache()
+
+    # the decoder layer's residual add + RMSNorm ahead of the block (qwen3_5.py:998-1004):
+    # lbmoe_forward_norm against lbmoe_forward on the normalised input, and against the
+    # reference's torch statements for the add and the norm followed by lbmoe_forward
+    name = "qwen3-30b-a3b decode + residual add + RMSNorm"
+    hid = make_x(g, 128, shape.hidden_size, device=dev)
+    res = make_x(g, 128, shape.hidden_size, device=dev)
+    nw = (make_x(g, 1, shape.hidden_size, device=dev)[0].float() * 0.1).to(torch.bfloat16)
+    if wanted(name):
+        out.append(norm_config(name, shape, hid, res, nw, steps, dev))
+    del hid, res, nw
 
     shape = SHAPES["qwen3-next-e512"]
     for fp8 in (False, True):

@@ -92,7 +92,8 @@ int32_t lbmoe_workspace_size(const lbmoe_layer* layer, int64_t T, size_t* bytes)
  * 4 counts int32 [E+1], 5 offsets int32 [E+2], 6 perm_tok int32 [T*k+T],
  * 7 perm_slot int32 [T*k], 8 inv int32 [T,k], 9 act bf16 [T*k+T, max(I,Is)]
  * (not written by the fp8 prefill path, whose gate_up stores the quantised act directly),
- * 10 expert_out bf16 [T*k+T, H]. */
+ * 10 expert_out bf16 [T*k+T, H], 11 xn bf16 [T,H] (the block input lbmoe_forward_norm
+ * computes). */
 int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t region,
                                size_t* offset, size_t* bytes);
 
@@ -102,6 +103,19 @@ int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t regi
  */
 int32_t lbmoe_forward(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The decoder layer's MLP half: qwen3_5.py:998-1004. hidden (the attention output) and
+ * residual are bf16 [T,H]; h = residual + hidden (bf16) is written to residual_out, and the
+ * block runs on x = Qwen3_5RMSNorm(h) (qwen3_5.py:39-55: fp32 h / sqrt(mean(h^2) + eps), times
+ * (1 + norm_weight), rounded to bf16; norm_weight bf16 [H]) into y bf16 [T,H]. For decode-sized
+ * T the add and the norm run inside the router kernel. residual_out must not overlap
+ * residual or hidden; x is kept in the workspace's xn region.
+ */
+int32_t lbmoe_forward_norm(const lbmoe_layer* layer, const void* hidden, const void* residual,
+                           const void* norm_weight, float eps, int64_t T, void* y,
+                           void* residual_out, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /* Number of events lbmoe_forward_profiled records. */
 #define LBMOE_PROFILE_EVENTS 7

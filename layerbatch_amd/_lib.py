@@ -19,7 +19,7 @@ LBMOE_W_FP8_E4M3 = 1
 
 REGIONS = {
     "logits": 0, "topk_idx": 1, "topk_w": 2, "shared_gate": 3, "counts": 4, "offsets": 5,
-    "perm_tok": 6, "perm_slot": 7, "inv": 8, "act": 9, "expert_out": 10,
+    "perm_tok": 6, "perm_slot": 7, "inv": 8, "act": 9, "expert_out": 10, "xn": 11,
 }
 
 _p = ctypes.c_void_p
@@ -51,6 +51,7 @@ _SIGS = {
     "lbmoe_workspace_region": (_i32, [_PL, _i64, _i32, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "lbmoe_forward": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p]),
     "lbmoe_forward_profiled": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p, ctypes.POINTER(_p), _i32]),
+    "lbmoe_forward_norm": (_i32, [_PL, _p, _p, _p, ctypes.c_float, _i64, _p, _p, _p, _sz, _p]),
     "lbmoe_router_logits": (_i32, [_PL, _p, _i64, _p, _p]),
     "lbmoe_route": (_i32, [_PL, _p, _p, _i64, _p, _i32, _p, _p, _p]),
     "lbmoe_permute_workspace_size": (_i32, [_i64, _i32, _i32, ctypes.POINTER(_sz)]),

@@ -32,6 +32,7 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
   w.bytes[R_INV] = V * 4;
   w.bytes[R_ACT] = Vs * Imax * 2;
   w.bytes[R_OUT] = Vs * H * 2;
+  w.bytes[R_XN] = T * H * 2;
   w.bytes[R_HIST] = E * nblk * 4;
   w.bytes[R_BASE] = E * nblk * 4;
   w.bytes[R_LRANK] = V * 4;
@@ -292,9 +293,17 @@ int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t regi
 
 namespace lbmoe {
 
+// The decoder layer's residual add + RMSNorm ahead of the block (lbmoe_forward_norm).
+struct NormArgs {
+  const void* residual;
+  const void* weight;
+  float eps;
+  void* residual_out;
+};
+
 static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                             void* workspace, size_t workspace_bytes, void* stream,
-                            StageEvents* ev) {
+                            StageEvents* ev, const NormArgs* norm = nullptr) {
   int32_t st = lbmoe_check_layer(layer);
   if (st != LBMOE_OK) return st;
   const lbmoe_layer& L = *layer;
@@ -312,7 +321,16 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
   void* topw = at<void>(ws, w, R_TOPW);
   float* sgate = sh ? at<float>(ws, w, R_SGATE) : nullptr;
   LBMOE_TRY(ev->mark(s));
-  LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
+  if (norm) {
+    // x is the attention output: the block's input is the normalised residual sum
+    void* xn = at<void>(ws, w, R_XN);
+    LBMOE_TRY(launch_add_rmsnorm_router(x, norm->residual, norm->weight, norm->eps, L.gate_weight,
+                                        T, L.num_experts, L.hidden_size, logits, xn,
+                                        norm->residual_out, s));
+    x = xn;
+  } else {
+    LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
+  }
   LBMOE_TRY(ev->mark(s));
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,
                               L.hidden_size, L.top_k, idx, 4, topw, sgate, s));
@@ -336,6 +354,19 @@ int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t 
   if (!events || n_events < LBMOE_PROFILE_EVENTS) return LBMOE_ERR_NULL;
   StageEvents ev{events, n_events, 0};
   return forward_impl(layer, x, T, y, workspace, workspace_bytes, stream, &ev);
+}
+
+int32_t lbmoe_forward_norm(const lbmoe_layer* layer, const void* hidden, const void* residual,
+                           const void* norm_weight, float eps, int64_t T, void* y,
+                           void* residual_out, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (T > 0 && (!hidden || !residual || !norm_weight || !residual_out)) return LBMOE_ERR_NULL;
+  // the fused router reads residual rows in several workgroups while others write residual_out
+  if (T > 0 && residual_out == residual) return LBMOE_ERR_SHAPE;
+  if (!(eps >= 0.f)) return LBMOE_ERR_SHAPE;
+  StageEvents none{nullptr, 0, 0};
+  const NormArgs norm{residual, norm_weight, eps, residual_out};
+  return forward_impl(layer, hidden, T, y, workspace, workspace_bytes, stream, &none, &norm);
 }
 
 int32_t lbmoe_router_logits(const lbmoe_layer* layer, const void* x, int64_t T, void* logits,

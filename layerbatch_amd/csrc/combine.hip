@@ -11,8 +11,11 @@
 
 namespace lbmoe {
 
-// One workgroup per token. The token's k (row, weight) pairs are read first, then every
-// thread issues its k row loads together before accumulating, so the loads overlap.
+// One workgroup per token. Per group of kCombineSlots slots, the token's (row, weight) pairs
+// are read first, then every thread issues its row loads together before accumulating, so the
+// loads overlap. All loads are unconditional (indices past k or rows of dropped pairs read a
+// real entry and are masked afterwards): a load under a condition would make the compiler
+// wait for every earlier load at the join.
 constexpr int kCombineSlots = 8;   // slots whose row loads are in flight together
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
@@ -27,21 +30,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < k; s0 += kCombineSlots) {
-      u32x4 o[kCombineSlots];
+      int p[kCombineSlots];
       float w[kCombineSlots];
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i) {
-        const int s = s0 + i;
-        const int p = s < k ? inv_t[s] : -1;
-        w[i] = p >= 0 ? bf2f(w_t[s]) : 0.f;
-        o[i] = p >= 0 ? ld16(rows + static_cast<int64_t>(p) * H + c) : u32x4{0, 0, 0, 0};
+        const int s = min(s0 + i, k - 1);
+        const bool in = s0 + i < k;
+        p[i] = in ? inv_t[s] : -1;
+        w[i] = bf2f(w_t[s]);
       }
+      u32x4 o[kCombineSlots];
+#pragma unroll
+      for (int i = 0; i < kCombineSlots; ++i)
+        o[i] = ld16(rows + static_cast<int64_t>(max(p[i], 0)) * H + c);
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i) {
+        const bool use = p[i] >= 0;        // dropped pairs and slots past k add nothing
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          acc[2 * q] += w[i] * bf_lo(o[i][q]);
-          acc[2 * q + 1] += w[i] * bf_hi(o[i][q]);
+          acc[2 * q] += use ? w[i] * bf_lo(o[i][q]) : 0.f;
+          acc[2 * q + 1] += use ? w[i] * bf_hi(o[i][q]) : 0.f;
         }
       }
     }

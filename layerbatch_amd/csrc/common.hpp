@@ -22,15 +22,17 @@ __device__ __forceinline__ float bf2f(uint16_t b) {
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Round-to-nearest-even float -> bf16 bits; NaN -> canonical quiet NaN.
+// Round-to-nearest-even float -> bf16 bits with v_cvt_pk_bf16_f32 (denormals kept; a NaN stays
+// a quiet NaN with its payload's top bits). The conversion of every non-NaN float equals the
+// textbook rounding (add 0x7fff plus the kept lowest bit, drop 16 bits): checked on the GPU
+// over every 997th fp32 bit pattern, all halfway cases and the denormals.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return f2bf(lo) | (f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 // Value of f after rounding to bf16.
 __device__ __forceinline__ float round_bf(float f) { return __uint_as_float(f2bf(f) << 16); }

@@ -109,11 +109,11 @@ __device__ __forceinline__ void f8_load(const uint8_t* const (&ap)[RA][4],
 #pragma unroll
   for (int i = 0; i < RA; ++i)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a[i][u] = ap[i][u] ? ld16_stream(ap[i][u] + k0) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u) a[i][u] = ld16_stream(ap[i][u] + k0);
 #pragma unroll
   for (int j = 0; j < TT; ++j)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) b[j][u] = bp[j][u] ? ld16(bp[j][u] + k0) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u) b[j][u] = ld16(bp[j][u] + k0);
 }
 
 __device__ __forceinline__ i32x8_t cat8(u32x4 lo, u32x4 hi) {
@@ -176,8 +176,8 @@ __device__ __forceinline__ void f8_dot(u32x4* __restrict__ lds, const uint8_t* c
     }
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
-      xsc[j][0] = xsp[j] ? xsp[j][sb] : 0.f;
-      xsc[j][1] = xsp[j] ? xsp[j][sb + 1] : 0.f;
+      xsc[j][0] = xsp[j][sb];
+      xsc[j][1] = xsp[j][sb + 1];
     }
     f8_mma<RA, TT>(lds, a, b, ws, xsc, acc);
 #pragma unroll
@@ -247,13 +247,13 @@ __global__ __launch_bounds__(64) void gate_up_fp8_kernel(GroupWeights gw, const 
     for (int j = 0; j < TT; ++j) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int p = p0 + 16 * j + 4 * u + q;
-        const int tok = p < n ? (shared ? p : perm_tok[row0 + p]) : -1;
-        bp[j][u] = tok >= 0 ? xq + static_cast<int64_t>(tok) * H + 16 * r : nullptr;
+        const int p = min(p0 + 16 * j + 4 * u + q, n - 1);   // past n: a real row, not stored
+        const int tok = shared ? p : perm_tok[row0 + p];
+        bp[j][u] = xq + static_cast<int64_t>(tok) * H + 16 * r;
       }
-      const int pc = p0 + 16 * j + r;     // this lane's accumulator column
-      const int tc = pc < n ? (shared ? pc : perm_tok[row0 + pc]) : -1;
-      xsp[j] = tc >= 0 ? xs + static_cast<int64_t>(tc) * nkb : nullptr;
+      const int pc = min(p0 + 16 * j + r, n - 1);          // this lane's accumulator column
+      const int tc = shared ? pc : perm_tok[row0 + pc];
+      xsp[j] = xs + static_cast<int64_t>(tc) * nkb;
     }
     f32x4 acc[2][TT];
     zero_acc8(acc);
@@ -311,11 +311,11 @@ __global__ __launch_bounds__(64) void down_fp8_kernel(GroupWeights gw, const uin
     for (int j = 0; j < TT; ++j) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int p = p0 + 16 * j + 4 * u + q;
-        bp[j][u] = p < n ? aq + static_cast<int64_t>(row0 + p) * act_ld + 16 * r : nullptr;
+        const int p = min(p0 + 16 * j + 4 * u + q, n - 1);   // past n: a real row, not stored
+        bp[j][u] = aq + static_cast<int64_t>(row0 + p) * act_ld + 16 * r;
       }
-      const int pc = p0 + 16 * j + r;
-      xsp[j] = pc < n ? as + static_cast<int64_t>(row0 + pc) * nsa : nullptr;
+      const int pc = min(p0 + 16 * j + r, n - 1);
+      xsp[j] = as + static_cast<int64_t>(row0 + pc) * nsa;
     }
     f32x4 acc[2][TT];
     zero_acc8(acc);

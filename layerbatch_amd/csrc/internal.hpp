@@ -18,12 +18,12 @@ inline int64_t perm_blocks(int64_t V) { return (V + kPermChunk - 1) / kPermChunk
 
 enum Region {
   R_LOGITS = 0, R_IDX, R_TOPW, R_SGATE, R_COUNTS, R_OFFSETS, R_PERM_TOK, R_PERM_SLOT, R_INV,
-  R_ACT, R_OUT,
+  R_ACT, R_OUT, R_XN,
   // private regions (not exposed through lbmoe_workspace_region)
   R_HIST, R_BASE, R_LRANK, R_TILES, R_XQ, R_XS, R_ACTQ, R_ACTS,
   R_COUNT_
 };
-constexpr int kPublicRegions = R_OUT + 1;
+constexpr int kPublicRegions = R_XN + 1;
 
 struct WsLayout {
   size_t off[R_COUNT_];
@@ -59,6 +59,12 @@ struct GroupWeights {
 // ---- launchers (each returns hipError_t of the launch) ----------------------------------
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
                                 void* logits, hipStream_t s);
+// Residual add + RMSNorm of the decoder layer ahead of the block, then the router logits of
+// its output: x_out = the block's input, res_out = the new residual (fused into the router
+// for decode-sized T).
+hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, const void* norm_w,
+                                     float eps, const void* wg, int64_t T, int E, int H,
+                                     void* logits, void* x_out, void* res_out, hipStream_t s);
 hipError_t launch_route_topk(const void* logits, const float* bias, const void* x,
                              const void* w_sg, int64_t T, int E, int H, int k, void* idx,
                              int idx_bytes, void* topw, float* sgate, hipStream_t s);

@@ -36,12 +36,12 @@ __device__ __forceinline__ void load_kblock(const uint16_t* const (&arow)[RA],
   for (int i = 0; i < RA; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      a[i][c] = arow[i] ? ld16_stream(arow[i] + k0 + 8 * c) : u32x4{0, 0, 0, 0};
+      a[i][c] = ld16_stream(arow[i] + k0 + 8 * c);
 #pragma unroll
   for (int j = 0; j < TT; ++j)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      b[j][c] = brow[j] ? ld16(brow[j] + k0 + 8 * c) : u32x4{0, 0, 0, 0};
+      b[j][c] = ld16(brow[j] + k0 + 8 * c);
 }
 
 template <int RA, int TT>
@@ -58,7 +58,10 @@ __device__ __forceinline__ void mma_kblock(const u32x4 (&a)[RA][4], const u32x4 
 }
 
 // acc[i][j] += W-tile i . X-tile j over NKB k-blocks (fully unrolled, kPD blocks in flight).
-// arow/brow are this lane's row pointers (nullptr = zero row), already offset by 32*q.
+// arow/brow are this lane's row pointers, already offset by 32*q. Every pointer must be valid:
+// loads are unconditional, so that the compiler can count the loads in flight exactly and keep
+// the prefetch; a padding row (a token past the group, say) points at a real row and its
+// output column is simply not stored.
 template <int RA, int TT, int NKB>
 __device__ __forceinline__ void stream_mma_fixed(const uint16_t* const (&arow)[RA],
                                                  const uint16_t* const (&brow)[TT],
@@ -126,11 +129,11 @@ __device__ __forceinline__ void wide_load(const uint16_t* const (&ap)[RA][4],
 #pragma unroll
   for (int i = 0; i < RA; ++i)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a[i][u] = ap[i][u] ? ld16_stream(ap[i][u] + k0) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u) a[i][u] = ld16_stream(ap[i][u] + k0);
 #pragma unroll
   for (int j = 0; j < TT; ++j)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) b[j][u] = bp[j][u] ? ld16(bp[j][u] + k0) : u32x4{0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u) b[j][u] = ld16(bp[j][u] + k0);
 }
 
 template <int RA, int TT>
@@ -163,8 +166,8 @@ __device__ __forceinline__ void wide_mma(u32x4* __restrict__ lds, const u32x4 (&
 }
 
 // acc += A . B^T over NKB k-blocks, kPD blocks of loads in flight (NKB = 0: rolled loop over K
-// with one block of lookahead). ap/bp are this lane's row pointers (nullptr = zero row),
-// already offset by its 16-byte chunk.
+// with one block of lookahead). ap/bp are this lane's row pointers, already offset by its
+// 16-byte chunk; all must be valid (padding rows point at real rows, their outputs unused).
 template <int RA, int TT, int NKB>
 __device__ __forceinline__ void wide_dot(u32x4* __restrict__ lds, const uint16_t* const (&ap)[RA][4],
                                          const uint16_t* const (&bp)[TT][4], int K,
@@ -210,39 +213,196 @@ static hipError_t with_nkb(int K, F&& f) {
   }
 }
 
+// ---- residual add + RMSNorm ahead of the block (qwen3_5.py:998-1002, :39-55) ---------------
+// h = bf16(residual + hidden) is the new residual; the block's input is
+// x = bf16((h * (1 / sqrt(mean(h^2) + eps))) * (1 + w_norm)), in fp32 as Qwen3_5RMSNorm does.
+
+// Elementwise h of 8 bf16 pairs; returns the sum of squares of the rounded values.
+__device__ __forceinline__ float add_bf8(const u32x4& a, const u32x4& b, u32x4& h) {
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = round_bf(bf_lo(a[j]) + bf_lo(b[j]));
+    const float hi = round_bf(bf_hi(a[j]) + bf_hi(b[j]));
+    h[j] = pack_bf2(lo, hi);
+    sq += lo * lo + hi * hi;
+  }
+  return sq;
+}
+__device__ __forceinline__ u32x4 norm_bf8(const u32x4& h, const u32x4& w, float rn) {
+  u32x4 x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    x[j] = pack_bf2((bf_lo(h[j]) * rn) * (1.0f + bf_lo(w[j])),
+                    (bf_hi(h[j]) * rn) * (1.0f + bf_hi(w[j])));
+  return x;
+}
+
+// One wave per token: h written to res_out, x to x_out.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __restrict__ hidden,
+                                                          const uint16_t* __restrict__ residual,
+                                                          const uint16_t* __restrict__ norm_w,
+                                                          float eps, int T, int H,
+                                                          uint16_t* __restrict__ x_out,
+                                                          uint16_t* __restrict__ res_out) {
+  const int lane = lane_id();
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int64_t row = static_cast<int64_t>(t) * H;
+  float sq = 0.f;
+  for (int k = 8 * lane; k < H; k += 8 * kWave) {
+    u32x4 h;
+    sq += add_bf8(ld16(residual + row + k), ld16(hidden + row + k), h);
+    *reinterpret_cast<u32x4*>(res_out + row + k) = h;
+  }
+  const float rn = 1.0f / sqrtf(wave_sum(sq) / static_cast<float>(H) + eps);
+  for (int k = 8 * lane; k < H; k += 8 * kWave) {
+    u32x4 h;
+    add_bf8(ld16(residual + row + k), ld16(hidden + row + k), h);
+    *reinterpret_cast<u32x4*>(x_out + row + k) = norm_bf8(h, ld16(norm_w + k), rn);
+  }
+}
+
 // ---- router logits: logits[t, e] = bf16(x[t] . Wg[e]) ----------------------------------
-// Workgroup = 4 waves on one 16-expert x 16-token tile, each wave a quarter of K; the four
-// partial sums are added in LDS (fixed order) and rounded once.
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ wg,
-                                                            int T, int E, int H,
-                                                            uint16_t* __restrict__ logits) {
-  __shared__ f32x4 part[3][64];
+// Decode sizes. Workgroup = 8 waves on one 16-expert x 16-token tile, wave w taking k-blocks
+// [nkb*w/8, nkb*(w+1)/8) of K (at most MAXB of them), so that every load of the wave is issued
+// before the first MFMA; the eight partial sums are added in LDS in a fixed order and
+// rounded once. NORM: x is not read but formed from the residual add and RMSNorm of the
+// decoder layer (below): each wave computes h and x for its k-blocks of the 16 token rows,
+// the waves' sums of squares meet in LDS, and the workgroups of expert tile 0 also store h
+// and x. Both variants run the same MFMA chains, so their logits are identical.
+constexpr int kRouterWaves = 8;
+struct NormIn {
+  const uint16_t* hidden;
+  const uint16_t* residual;
+  const uint16_t* weight;
+  float eps;
+  uint16_t* x_out;
+  uint16_t* res_out;
+};
+
+template <bool NORM, int MAXB>
+__global__ __launch_bounds__(64 * kRouterWaves) void router_logits_kernel(
+    const uint16_t* __restrict__ x, NormIn nm, const uint16_t* __restrict__ wg, int T, int E,
+    int H, uint16_t* __restrict__ logits) {
+  __shared__ f32x4 part[kRouterWaves - 1][64];
+  __shared__ float ss[kRouterWaves][16];
   const int lane = lane_id(), r = lane & 15, q = lane >> 4, w = threadIdx.x >> 6;
   const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
   const int nkb = H / kKBlock;
-  const int kb0 = (nkb * w) / 4, kb1 = (nkb * (w + 1)) / 4;
-  f32x4 acc[1][1];
-  zero_acc(acc);
-  if (kb1 > kb0) {
-    const int koff = kb0 * kKBlock + 32 * q;
-    const uint16_t* arow[1] = {e0 + r < E ? wg + static_cast<int64_t>(e0 + r) * H + koff : nullptr};
-    const uint16_t* brow[1] = {t0 + r < T ? x + static_cast<int64_t>(t0 + r) * H + koff : nullptr};
-    stream_mma<1, 1>(arow, brow, (kb1 - kb0) * kKBlock, acc);
-  }
-  if (w > 0) part[w - 1][lane] = acc[0][0];
-  __syncthreads();
-  if (w != 0) return;
-  f32x4 s = acc[0][0];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) s += part[i][lane];
+  const int kb0 = (nkb * w) / kRouterWaves, nb = (nkb * (w + 1)) / kRouterWaves - kb0;
   const int t = t0 + r;
-  if (t >= T) return;
+  const bool tv = t < T;
+  // rows past T or E are loaded from the last real row (loads stay unconditional, so the
+  // compiler keeps them all in flight) and their results are not stored
+  const int64_t row = static_cast<int64_t>(min(t, T - 1)) * H;
+  const uint16_t* wrow = wg + static_cast<int64_t>(min(e0 + r, E - 1)) * H;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto mfma_blocks = [&](const u32x4 (&a)[MAXB][4], const u32x4 (&b)[MAXB][4], int n) {
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      if (i >= n) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i][c]), as_bf16x8(b[i][c]), acc,
+                                                      0, 0, 0);
+    }
+  };
+  if constexpr (NORM) {
+    // one pass (the host guarantees nb <= MAXB); every wave reaches the barrier, also one
+    // without k-blocks
+    u32x4 a[MAXB][4], b[MAXB][4], c2[MAXB][4], nwv[MAXB][4];
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      if (i >= nb) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = (kb0 + i) * kKBlock + 32 * q + 8 * c;
+        a[i][c] = ld16_stream(wrow + k);
+        b[i][c] = ld16(nm.residual + row + k);
+        c2[i][c] = ld16(nm.hidden + row + k);
+        nwv[i][c] = ld16(nm.weight + k);
+      }
+    }
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      if (i >= nb) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sq += add_bf8(b[i][c], c2[i][c], b[i][c]);     // b := h
+    }
+    sq += __shfl_xor(sq, 16, kWave);
+    sq += __shfl_xor(sq, 32, kWave);
+    if (q == 0) ss[w][r] = sq;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int v = 0; v < kRouterWaves; ++v) tot += ss[v][r];
+    const float rn = 1.0f / sqrtf(tot / static_cast<float>(H) + nm.eps);
+    const bool store = blockIdx.x == 0 && tv;
+#pragma unroll
+    for (int i = 0; i < MAXB; ++i) {
+      if (i >= nb) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = (kb0 + i) * kKBlock + 32 * q + 8 * c;
+        if (store) *reinterpret_cast<u32x4*>(nm.res_out + row + k) = b[i][c];
+        b[i][c] = norm_bf8(b[i][c], nwv[i][c], rn);                                // b := x
+        if (store) *reinterpret_cast<u32x4*>(nm.x_out + row + k) = b[i][c];
+      }
+    }
+    mfma_blocks(a, b, nb);
+  } else {
+    // MAXB k-blocks per pass, every operand of a pass loaded before its first MFMA
+    for (int base = 0; base < nb; base += MAXB) {
+      u32x4 a[MAXB][4], b[MAXB][4];
+#pragma unroll
+      for (int i = 0; i < MAXB; ++i) {
+        if (base + i >= nb) break;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int k = (kb0 + base + i) * kKBlock + 32 * q + 8 * c;
+          a[i][c] = ld16_stream(wrow + k);
+          b[i][c] = ld16(x + row + k);
+        }
+      }
+      mfma_blocks(a, b, nb - base);
+    }
+  }
+  if (w > 0) part[w - 1][lane] = acc;
+  __syncthreads();
+  if (w != 0 || !tv) return;
+  f32x4 sum = acc;
+#pragma unroll
+  for (int i = 0; i < kRouterWaves - 1; ++i) sum += part[i][lane];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int e = e0 + 4 * q + v;
-    if (e < E) logits[static_cast<int64_t>(t) * E + e] = static_cast<uint16_t>(f2bf(s[v]));
+    if (e < E) logits[static_cast<int64_t>(t) * E + e] = static_cast<uint16_t>(f2bf(sum[v]));
   }
+}
+
+// Per-wave k-blocks the decode router keeps in registers at once: up to 4 per pass; the fused
+// norm needs all of a wave's blocks in one pass and fits 2 (H <= 2048) without spilling.
+constexpr int kRouterPassBlocks = 4;
+constexpr int kRouterNormBlocks = 2;
+
+template <bool NORM>
+static hipError_t launch_router_decode(const uint16_t* x, const NormIn& nm, const void* wg,
+                                       int64_t T, int E, int H, void* logits, hipStream_t s) {
+  const dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
+  const int per_wave = (H / kKBlock + kRouterWaves - 1) / kRouterWaves;
+  const auto* w = static_cast<const uint16_t*>(wg);
+  auto* lg = static_cast<uint16_t*>(logits);
+  const int Ti = static_cast<int>(T);
+#define LBMOE_ROUTER(B) \
+  router_logits_kernel<NORM, B><<<grid, 64 * kRouterWaves, 0, s>>>(x, nm, w, Ti, E, H, lg)
+  if (per_wave <= 1) LBMOE_ROUTER(1);
+  else if constexpr (NORM) LBMOE_ROUTER(kRouterNormBlocks);
+  else if (per_wave <= 2) LBMOE_ROUTER(2);
+  else LBMOE_ROUTER(kRouterPassBlocks);
+#undef LBMOE_ROUTER
+  return hipGetLastError();
 }
 
 // Token count from which the router logits run as an LDS-tiled MFMA GEMM.
@@ -252,12 +412,24 @@ hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E,
                                 void* logits, hipStream_t s) {
   if (T >= kTiledRouterMinTokens && tiled_router_supported(E, H))
     return launch_router_logits_tiled(x, wg, T, E, H, logits, s);
-  const dim3 grid((E + 15) / 16, static_cast<unsigned>((T + 15) / 16));
-  router_logits_kernel<<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x),
-                                            static_cast<const uint16_t*>(wg),
-                                            static_cast<int>(T), E, H,
-                                            static_cast<uint16_t*>(logits));
-  return hipGetLastError();
+  return launch_router_decode<false>(static_cast<const uint16_t*>(x), NormIn{}, wg, T, E, H,
+                                     logits, s);
+}
+
+hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, const void* norm_w,
+                                     float eps, const void* wg, int64_t T, int E, int H,
+                                     void* logits, void* x_out, void* res_out, hipStream_t s) {
+  const NormIn nm{static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(residual),
+                  static_cast<const uint16_t*>(norm_w), eps, static_cast<uint16_t*>(x_out),
+                  static_cast<uint16_t*>(res_out)};
+  const int per_wave = (H / kKBlock + kRouterWaves - 1) / kRouterWaves;
+  if (T < kTiledRouterMinTokens && per_wave <= kRouterNormBlocks)
+    return launch_router_decode<true>(nullptr, nm, wg, T, E, H, logits, s);
+  add_rmsnorm_kernel<<<static_cast<unsigned>((T + 3) / 4), 256, 0, s>>>(
+      nm.hidden, nm.residual, nm.weight, eps, static_cast<int>(T), H, nm.x_out, nm.res_out);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_router_logits(x_out, wg, T, E, H, logits, s);
 }
 
 // Token tiles per pass from the expected tokens per routed expert (T*k/E): enough columns
@@ -314,9 +486,9 @@ __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
     for (int j = 0; j < TT; ++j)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int p = p0 + 16 * j + 4 * u + q;
-        const int tok = p < n ? (shared ? p : perm_tok[row0 + p]) : -1;
-        bp[j][u] = tok >= 0 ? x + static_cast<int64_t>(tok) * H + 8 * r : nullptr;
+        const int p = min(p0 + 16 * j + 4 * u + q, n - 1);   // past n: a real row, not stored
+        const int tok = shared ? p : perm_tok[row0 + p];
+        bp[j][u] = x + static_cast<int64_t>(tok) * H + 8 * r;
       }
     f32x4 acc[2][TT];
     zero_acc(acc);
@@ -395,8 +567,8 @@ __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
     for (int j = 0; j < TT; ++j)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int p = p0 + 16 * j + 4 * u + q;
-        bp[j][u] = p < n ? act + static_cast<int64_t>(row0 + p) * act_ld + 8 * r : nullptr;
+        const int p = min(p0 + 16 * j + 4 * u + q, n - 1);   // past n: a real row, not stored
+        bp[j][u] = act + static_cast<int64_t>(row0 + p) * act_ld + 8 * r;
       }
     f32x4 acc[2][TT];
     zero_acc(acc);

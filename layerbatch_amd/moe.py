@@ -271,6 +271,35 @@ class Qwen3_5SparseMoeBlock(nn.Module):
                   "lbmoe_forward")
         return y
 
+    def forward_norm(self, hidden_states: torch.Tensor, residual: torch.Tensor, norm,
+                     workspace: torch.Tensor = None):
+        """The decoder layer's MLP half in one call (qwen3_5.py:998-1004):
+
+            hidden_states = residual + hidden_states; residual = hidden_states
+            hidden_states = norm(hidden_states); hidden_states = self(hidden_states)
+
+        norm is the layer's post_attention_layernorm (a Qwen3_5RMSNorm: ``weight`` [H] and
+        ``eps``). Returns (block output, new residual); the inputs are not modified.
+        """
+        _require(hidden_states, "hidden_states", ndim=2)
+        _require(residual, "residual", ndim=2)
+        _require(norm.weight, "norm.weight", ndim=1)
+        if residual.shape != hidden_states.shape:
+            raise RuntimeError("hidden_states and residual must have the same shape")
+        T = hidden_states.shape[0]
+        L = self.layer()
+        dev = hidden_states.device
+        if workspace is None:
+            workspace = _workspace(L, T, dev)
+        y = torch.empty_like(hidden_states)
+        new_residual = torch.empty_like(residual)
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_forward_norm(ctypes.byref(L), ptr(hidden_states), ptr(residual),
+                                           ptr(norm.weight), float(norm.eps), T, ptr(y),
+                                           ptr(new_residual), ptr(workspace), workspace.numel(),
+                                           _lib.stream_of(dev)), "lbmoe_forward_norm")
+        return y, new_residual
+
     @torch.no_grad()
     def quantize_fp8_(self):
         """Convert expert (and shared-expert) weights to e4m3fn + 128x128 block scales."""

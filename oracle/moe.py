@@ -10,6 +10,9 @@ Restates nanovllm/models/qwen3_5.py:754-917 on the CPU:
                                   Qwen3_5SharedExpertMLP + shared_expert_gate,
                                   qwen3_5.py:897, :903, :916-917
 * ``block_forward``               Qwen3_5SparseMoeBlock.forward, qwen3_5.py:899-905
+* ``add_rmsnorm``                 the decoder layer's residual add and post-attention
+                                  Qwen3_5RMSNorm ahead of the MoE block, qwen3_5.py:998-1002,
+                                  :39-55
 * ``quant_blocks`` / ``quant_groups`` / ``experts_fp8`` / ``block_forward_fp8``
                                   the fp8-e4m3 variant, which has no counterpart in the
                                   reference (no fp8 code exists there); defined here by
@@ -37,6 +40,9 @@ tests/test_oracle.py and tests/test_golden.py):
   independent torch float64 path; linearity in w_down and in the routing weights;
   T = 1 as k independent GEMVs; the torch-CPU restatement of both reference algorithms
   (oracle/torch_ref.py) within bf16 tolerance.
+* add_rmsnorm: torch's restatement of Qwen3_5RMSNorm within one bf16 step; closed forms
+  (a constant row normalises to its sign; with eps = 0, scaling a row by a power of two
+  leaves the output unchanged; weight w scales by (1 + w)).
 * fp8 functions: quantise/dequantise round trips, exactness on e4m3-representable blocks,
   scale closed forms, and the bf16 oracle within fp8 error bounds.
 * the reference module itself: tests/golden/reference_moe_small.npz holds outputs recorded
@@ -52,7 +58,7 @@ __all__ = [
     "router_logits", "route", "route_by_prob", "shared_gate", "permute", "experts",
     "shared_expert", "block_forward", "silu", "quant_blocks", "dequant_blocks",
     "quant_groups", "dequant_groups", "experts_fp8", "shared_expert_fp8",
-    "block_forward_fp8", "rel_err",
+    "block_forward_fp8", "rel_err", "add_rmsnorm",
 ]
 
 
@@ -284,3 +290,19 @@ def block_forward_fp8(x, wg, k, q, bias=None):
         y = y + g[:, None] * shared_expert_fp8(x, q["sh_gate_q"], q["sh_gate_s"], q["sh_up_q"],
                                                q["sh_up_s"], q["sh_down_q"], q["sh_down_s"])
     return y, w, idx
+
+
+def add_rmsnorm(hidden, residual, weight, eps):
+    """The MoE block's input in the decoder layer: qwen3_5.py:998-1002.
+
+    h = bf16(residual + hidden) (bf16 tensors add in fp32 and round, :998); the new residual is
+    h (:1001); x = Qwen3_5RMSNorm(h) (:1002, :39-55): in fp32, h * 1/sqrt(mean(h^2) + eps),
+    then times (1 + weight), rounded to bf16. hidden, residual [T,H] and weight [H] hold bf16
+    values. Returns (h, x) as float32 arrays of bf16 values.
+    """
+    h = bf16_round((np.asarray(residual, np.float32) + np.asarray(hidden, np.float32)).astype(np.float32))
+    ms = np.mean(h * h, axis=-1, keepdims=True, dtype=np.float32)
+    r = (np.float32(1.0) / np.sqrt(ms + np.float32(eps))).astype(np.float32)
+    one_w = (np.float32(1.0) + np.asarray(weight, np.float32)).astype(np.float32)
+    x = bf16_round(((h * r).astype(np.float32) * one_w).astype(np.float32))
+    return h, x

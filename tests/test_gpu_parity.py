@@ -9,6 +9,7 @@ from layerbatch_amd import _lib
 from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
 from layerbatch_amd.synth import MoEShape, SHAPES, make_layer, make_x, zipf_bias
 from oracle import moe as om
+from oracle.codecs import bf16_bits
 from tests import gpu_checks as gc
 from tests.helpers import bf16_bits_of, layer_np, to_np
 
@@ -238,3 +239,54 @@ def test_route_ties(gpu, T, E, k, levels, bias):
     ln = to_np(zb)
     ln = np.where(np.isnan(ln), -np.inf, ln)   # the oracle's view of a NaN logit
     gc.check_route(to_np(idx), bf16_bits_of(w), ln, b_np, k)
+
+
+class _Norm(torch.nn.Module):
+    """Stand-in for the layer's post_attention_layernorm (Qwen3_5RMSNorm: weight [H], eps)."""
+
+    def __init__(self, w, eps):
+        super().__init__()
+        self.weight = torch.nn.Parameter(w, requires_grad=False)
+        self.eps = eps
+
+
+@pytest.mark.parametrize("shape_name,T", [("small-h1024-e16", 40), ("qwen3-30b-a3b", 128),
+                                          ("qwen3-30b-a3b", 1), ("qwen3-next-e512", 1100)])
+def test_forward_norm(gpu, shape_name, T):
+    """Residual add + RMSNorm + block (qwen3_5.py:998-1004): the new residual is the bf16 sum
+    bit for bit, the block input within one bf16 step of the oracle's Qwen3_5RMSNorm, and the
+    output equals the plain block on that input bit for bit (decode T: norm fused into the
+    router kernel; T >= 1024: separate norm kernel)."""
+    shape = SHAPES[shape_name]
+    H = shape.hidden_size
+    w, g = make_layer(shape, seed=T, device=gpu)
+    blk = _block(shape, w, gpu)
+    hid = make_x(g, T, H, device=gpu)
+    res = (make_x(g, T, H, device=gpu).float() * 3).to(torch.bfloat16)
+    norm = _Norm((make_x(g, 1, H, device=gpu)[0].float() * 0.1).to(torch.bfloat16), 1e-6)
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=gpu)
+    y, new_res = blk.forward_norm(hid, res, norm, workspace=ws)
+    torch.cuda.synchronize()
+    h_ref, x_ref = om.add_rmsnorm(to_np(hid), to_np(res), to_np(norm.weight), 1e-6)
+    np.testing.assert_array_equal(to_np(new_res), h_ref)
+    xn = _region(blk, ws, T, "xn", torch.bfloat16, (T, H)).clone()
+    d = np.abs(bf16_bits_of(xn).astype(np.int32) - bf16_bits(x_ref).astype(np.int32))
+    assert d.max() <= 1, f"block input differs from the oracle's RMSNorm by {d.max()} bf16 steps"
+    y_plain = blk(xn)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_plain)
+
+
+def test_forward_norm_rejects_in_place_residual(gpu, lbmoe):
+    shape = SHAPES["small-h1024-e16"]
+    w, g = make_layer(shape, seed=2, device=gpu)
+    blk = _block(shape, w, gpu)
+    L = blk.layer()
+    hid = make_x(g, 8, 1024, device=gpu)
+    res = make_x(g, 8, 1024, device=gpu)
+    nw = torch.zeros(1024, dtype=torch.bfloat16, device=gpu)
+    y = torch.empty_like(hid)
+    ws = torch.empty(blk.workspace_size(8), dtype=torch.uint8, device=gpu)
+    st = lbmoe.lbmoe_forward_norm(ctypes.byref(L), _lib.ptr(hid), _lib.ptr(res), _lib.ptr(nw), 1e-6, 8,
+                                  _lib.ptr(y), _lib.ptr(res), _lib.ptr(ws), ws.numel(), _lib.stream_of(gpu))
+    assert st == -2

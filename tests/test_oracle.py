@@ -281,3 +281,51 @@ def test_zipf_bias_skews_load():
     p = np.exp(b)
     assert abs(p.sum() - 1) < 1e-5
     assert sorted(p)[::-1][0] / sorted(p)[::-1][-1] > 300
+
+
+# ---- residual add + RMSNorm ahead of the block ------------------------------------------------
+
+def _torch_add_rmsnorm(hid, res, w, eps):
+    """The reference's statements (qwen3_5.py:998, :1002 with Qwen3_5RMSNorm :48-55) in torch."""
+    h = res + hid                                         # bf16 + bf16 -> bf16
+    out = h.float()
+    out = out * torch.rsqrt(out.pow(2).mean(-1, keepdim=True) + eps)
+    out = out * (1.0 + w.float())
+    return h, out.type_as(h)
+
+
+@pytest.mark.parametrize("H,eps", [(2048, 1e-6), (1024, 1e-5), (256, 1e-6)])
+def test_add_rmsnorm_matches_torch(H, eps):
+    g = torch.Generator().manual_seed(H)
+    hid = torch.randn((64, H), generator=g).to(torch.bfloat16)
+    res = (torch.randn((64, H), generator=g) * 4).to(torch.bfloat16)
+    w = (torch.randn(H, generator=g) * 0.1).to(torch.bfloat16)
+    h_t, x_t = _torch_add_rmsnorm(hid, res, w, eps)
+    h, x = om.add_rmsnorm(to_np(hid), to_np(res), to_np(w), eps)
+    np.testing.assert_array_equal(codecs.bf16_bits(h), to_np(h_t.view(torch.int16)).view(np.uint16))
+    d = np.abs(codecs.bf16_bits(x).astype(np.int32) - to_np(x_t.view(torch.int16)).view(np.uint16).astype(np.int32))
+    assert d.max() <= 1, f"RMSNorm differs from torch by {d.max()} bf16 steps"
+    assert (d == 0).mean() > 0.99
+
+
+def test_add_rmsnorm_closed_forms():
+    H = 512
+    rng = np.random.default_rng(3)
+    # a constant row normalises to its sign (eps = 0)
+    c = codecs.bf16_round(rng.standard_normal(8).astype(np.float32) * 5)
+    hid = np.repeat(c[:, None], H, axis=1).astype(np.float32)
+    _, x = om.add_rmsnorm(hid, np.zeros_like(hid), np.zeros(H, np.float32), 0.0)
+    np.testing.assert_array_equal(x, np.sign(hid))
+    # eps = 0: scaling both inputs by a power of two leaves the output unchanged
+    hid = codecs.bf16_round(rng.standard_normal((16, H)).astype(np.float32))
+    res = codecs.bf16_round(rng.standard_normal((16, H)).astype(np.float32))
+    w = codecs.bf16_round((rng.standard_normal(H) * 0.2).astype(np.float32))
+    h1, x1 = om.add_rmsnorm(hid, res, w, 0.0)
+    h8, x8 = om.add_rmsnorm(hid * 8, res * 8, w, 0.0)
+    np.testing.assert_array_equal(h8, h1 * 8)
+    np.testing.assert_array_equal(x8, x1)
+    # weight 1 doubles the weight-0 output exactly; the residual add is the bf16 sum
+    _, x0 = om.add_rmsnorm(hid, res, np.zeros(H, np.float32), 1e-6)
+    _, x2 = om.add_rmsnorm(hid, res, np.ones(H, np.float32), 1e-6)
+    np.testing.assert_array_equal(x2, 2 * x0)
+    np.testing.assert_array_equal(h1, codecs.bf16_round((hid + res).astype(np.float32)))
