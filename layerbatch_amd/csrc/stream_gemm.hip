@@ -2,215 +2,159 @@
 //
 // Every GEMM of the layer has the form C[rows of W, tokens] = W[rows, K] . X[tokens, K]^T
 // with both operands K-contiguous (the reference's nn.Linear / 3-D expert layouts,
-// nanovllm/models/qwen3_5.py:765, :795-800, :912-914). A wave owns 16*RA weight rows and
-// streams them from HBM once per pass over its group's tokens; the tokens (16 per MFMA
-// column tile, TT tiles per pass) are read through L2. This is the decode-sized regime,
-// where the layer is bound by streaming each hit expert's weights once.
+// nanovllm/models/qwen3_5.py:765, :795-800, :912-914). This is the decode-sized regime, where
+// the layer is bound by streaming each hit expert's weights from HBM once.
 //
-// MFMA operand mapping. For v_mfma_f32_16x16x32_bf16 lane l = 16*q + r supplies row r of A
-// and column r of B, 8 consecutive k each. K is walked in blocks of 128: in block kb lane
-// (r, q) loads the 64 contiguous bytes k in [kb + 32q, kb + 32q + 32) of its weight row and
-// of its token row, and MFMA c (c = 0..3) consumes the c-th 8-element chunk. A and B use the
-// same (lane, chunk) -> k map, so the products pair correctly and each weight row is read
-// as 256-byte contiguous segments. Accumulator lane (r, q) holds rows 4q..4q+3 of column r.
+// Split-K workgroups. A workgroup of W waves owns one item: 32 weight rows (two 16-row MFMA
+// tiles) of one group against all of the group's tokens (16 per MFMA column tile, TT tiles per
+// pass). Wave w streams k-blocks [w*per, (w+1)*per) of the 32 rows, per = K/128/W, issuing all
+// loads of MAXB k-blocks before its first MFMA, so the item's 32 x K weight block is in flight
+// at once, as one burst of neighbouring addresses. HBM streams such bursts markedly faster
+// than one long per-wave stream per row block (a bandwidth probe: 6.5-6.9 TB/s against
+// 5.7-6.2 TB/s over 0.75-1.5 GB). The W partial sums meet in LDS and are added in wave order,
+// a fixed order, so results do not depend on timing.
 //
-// Loads run kPD k-blocks ahead of the MFMAs. When K/128 is one of the unrolled sizes the
-// whole K loop is unrolled so that the load of block i+kPD and the MFMAs of block i are
-// statically scheduled; other sizes use a rolled loop with one block of lookahead.
+// Wide loads. One load instruction covers 4 rows x 256 contiguous bytes (16 lanes per row,
+// 16 bytes each): lane l holds row 4u + l/16 (u = instruction), chunk l%16 of the row's
+// 128-element k-block. v_mfma_f32_16x16x32_bf16 wants row r in lane r (mod 16), so each 16 x
+// 128 tile passes through a private 4 KB LDS slot of the wave: chunk j of row R sits at slot
+// 16R + (j ^ (R & 15)), free of bank conflicts for both the 16-lane row writes and the 16-row
+// column reads. MFMA c of a k-block consumes chunks 4c..4c+3: lane (r, q) gets chunk 4c + q of
+// row r, k = kb + 32c + 8q .. +8, for both operands, so the products pair correctly. A wave's
+// LDS operations execute in issue order, so the slot is reused tile after tile without waits.
+// Accumulator lane (r, q) holds rows 4q..4q+3 of column r.
 #include "common.hpp"
 #include "internal.hpp"
 
 namespace lbmoe {
 
 constexpr int kKBlock = 128;
-#ifndef LBMOE_STREAM_PD
-#define LBMOE_STREAM_PD 2
-#endif
-constexpr int kPD = LBMOE_STREAM_PD;   // k-blocks of loads in flight ahead of the MFMAs
+constexpr int kSplitMaxWaves = 8;
 
-template <int RA, int TT>
-__device__ __forceinline__ void load_kblock(const uint16_t* const (&arow)[RA],
-                                            const uint16_t* const (&brow)[TT], int k0,
-                                            u32x4 (&a)[RA][4], u32x4 (&b)[TT][4]) {
+// LDS of a split-K workgroup, in 16-byte units: the waves' transpose slots, later reused for
+// the partial sums [wave][tile i][token tile j][lane].
+template <int TT>
+constexpr int split_lds_u4() {
+  return kSplitMaxWaves * 256 > kSplitMaxWaves * 2 * TT * 64 ? kSplitMaxWaves * 256
+                                                               : kSplitMaxWaves * 2 * TT * 64;
+}
+
+// Loads k-block kb of both weight tiles and of the TT token tiles. abase[i] is tile i's
+// wave-uniform base, astep the uniform byte step between load instructions (4 rows) and aoff
+// this lane's 32-bit byte offset, so the weight loads take the scalar-base form. Every pointer must be valid: padding token rows point at real rows and
+// their outputs are not stored, so the loads stay unconditional and the compiler can count
+// those in flight exactly.
+template <int TT>
+__device__ __forceinline__ void split_load(const char* const (&abase)[2], int astep, uint32_t aoff,
+                                           const uint16_t* const (&bp)[TT][4], int kb,
+                                           u32x4 (&a)[2][4], u32x4 (&b)[TT][4]) {
+  const int kbyte = kb * kKBlock * 2;
 #pragma unroll
-  for (int i = 0; i < RA; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      a[i][c] = ld16_stream(arow[i] + k0 + 8 * c);
+    for (int u = 0; u < 4; ++u) a[i][u] = ld16_stream(abase[i] + (kbyte + u * astep) + aoff);
 #pragma unroll
   for (int j = 0; j < TT; ++j)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      b[j][c] = ld16(brow[j] + k0 + 8 * c);
+    for (int u = 0; u < 4; ++u) b[j][u] = ld16(bp[j][u] + kb * kKBlock);
 }
 
-template <int RA, int TT>
-__device__ __forceinline__ void mma_kblock(const u32x4 (&a)[RA][4], const u32x4 (&b)[TT][4],
-                                           f32x4 (&acc)[RA][TT]) {
+// acc += A . B^T over one k-block, each tile transposed through the wave's LDS slot. The
+// token tiles go first and each weight tile's MFMAs follow its transpose, so that few
+// fragments are live next to the loads still in flight.
+template <int TT>
+__device__ __forceinline__ void split_mma(u32x4* __restrict__ slot, const u32x4 (&a)[2][4],
+                                          const u32x4 (&b)[TT][4], f32x4 (&acc)[2][TT]) {
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+  auto transpose = [&](const u32x4 (&t)[4], u32x4 (&f)[4]) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+    for (int u = 0; u < 4; ++u) slot[(4 * u + q) * 16 + (r ^ (4 * u + q))] = t[u];
 #pragma unroll
-    for (int i = 0; i < RA; ++i)
+    for (int c = 0; c < 4; ++c) f[c] = slot[r * 16 + ((4 * c + q) ^ r)];
+  };
+  u32x4 fb[TT][4];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) transpose(b[j], fb[j]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    u32x4 fa[4];
+    transpose(a[i], fa);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int j = 0; j < TT; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i][c]), as_bf16x8(b[j][c]),
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[c]), as_bf16x8(fb[j][c]),
                                                             acc[i][j], 0, 0, 0);
-}
-
-// acc[i][j] += W-tile i . X-tile j over NKB k-blocks (fully unrolled, kPD blocks in flight).
-// arow/brow are this lane's row pointers, already offset by 32*q. Every pointer must be valid:
-// loads are unconditional, so that the compiler can count the loads in flight exactly and keep
-// the prefetch; a padding row (a token past the group, say) points at a real row and its
-// output column is simply not stored.
-template <int RA, int TT, int NKB>
-__device__ __forceinline__ void stream_mma_fixed(const uint16_t* const (&arow)[RA],
-                                                 const uint16_t* const (&brow)[TT],
-                                                 f32x4 (&acc)[RA][TT]) {
-  u32x4 a[NKB][RA][4], b[NKB][TT][4];
-#pragma unroll
-  for (int p = 0; p < kPD && p < NKB; ++p) load_kblock<RA, TT>(arow, brow, p * kKBlock, a[p], b[p]);
-#pragma unroll
-  for (int i = 0; i < NKB; ++i) {
-    if (i + kPD < NKB) load_kblock<RA, TT>(arow, brow, (i + kPD) * kKBlock, a[i + kPD], b[i + kPD]);
-    mma_kblock<RA, TT>(a[i], b[i], acc);
   }
 }
 
-// Rolled variant for any K (multiple of 128), one block of lookahead.
-template <int RA, int TT>
-__device__ __forceinline__ void stream_mma(const uint16_t* const (&arow)[RA],
-                                           const uint16_t* const (&brow)[TT], int K,
-                                           f32x4 (&acc)[RA][TT]) {
-  u32x4 a[RA][4], b[TT][4], an[RA][4], bn[TT][4];
-  load_kblock<RA, TT>(arow, brow, 0, a, b);
-  for (int kb = 0; kb < K; kb += kKBlock) {
-    if (kb + kKBlock < K) load_kblock<RA, TT>(arow, brow, kb + kKBlock, an, bn);
-    mma_kblock<RA, TT>(a, b, acc);
+// This wave's share of the item: acc = sum over k-blocks [kb0, kb0 + per) in chunks of MAXB.
+// ALL_FIRST issues every load of a chunk before its first MFMA at the cost of occupancy,
+// which pays off for down with two token tiles (80 instead of 111 us at 256 tokens); elsewhere
+// the compiler's interleaving at higher occupancy is faster.
+template <int TT, int MAXB, bool ALL_FIRST>
+__device__ __forceinline__ void split_dot(u32x4* __restrict__ slot, const char* const (&abase)[2],
+                                          int astep, uint32_t aoff,
+                                          const uint16_t* const (&bp)[TT][4], int kb0, int per,
+                                          f32x4 (&acc)[2][TT]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-#pragma unroll
-      for (int i = 0; i < RA; ++i) a[i][c] = an[i][c];
-#pragma unroll
-      for (int j = 0; j < TT; ++j) b[j][c] = bn[j][c];
-    }
-  }
-}
-
-// NKB = 0 selects the rolled loop over K.
-template <int RA, int TT, int NKB>
-__device__ __forceinline__ void stream_dot(const uint16_t* const (&arow)[RA],
-                                           const uint16_t* const (&brow)[TT], int K,
-                                           f32x4 (&acc)[RA][TT]) {
-  if constexpr (NKB > 0) stream_mma_fixed<RA, TT, NKB>(arow, brow, acc);
-  else stream_mma<RA, TT>(arow, brow, K, acc);
-}
-
-template <int RA, int TT>
-__device__ __forceinline__ void zero_acc(f32x4 (&acc)[RA][TT]) {
-#pragma unroll
-  for (int i = 0; i < RA; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < TT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-}
-
-// ---- wide loads + per-wave LDS transpose ---------------------------------------------------
-// HBM streams best when each load instruction covers few rows with long contiguous runs. Here
-// one instruction loads 4 rows x 256 contiguous bytes (16 lanes per row, 16 bytes each): lane l
-// holds row 4u + l/16 (u = instruction), chunk l%16 of the row's 128-element k-block. The MFMA
-// needs row r in lane r (mod 16), so each wave writes its k-block to a private LDS scratch and
-// reads it back transposed. Chunk j of scratch row R sits at slot 16R + (j ^ (R & 15)), which
-// keeps both the 16-lane row writes and the 16-row column reads free of bank conflicts.
-// MFMA c of a k-block consumes chunks 4c..4c+3: lane (r, q) gets chunk 4c + q of row r, i.e.
-// k = kb + 32c + 8q .. +8 for both operands.
-template <int RA, int TT>
-__device__ __forceinline__ void wide_load(const uint16_t* const (&ap)[RA][4],
-                                          const uint16_t* const (&bp)[TT][4], int k0,
-                                          u32x4 (&a)[RA][4], u32x4 (&b)[TT][4]) {
+  for (int kb = kb0; kb < kb0 + per; kb += MAXB) {
+    u32x4 a[MAXB][2][4], b[MAXB][TT][4];
 #pragma unroll
-  for (int i = 0; i < RA; ++i)
+    for (int m = 0; m < MAXB; ++m) split_load<TT>(abase, astep, aoff, bp, kb + m, a[m], b[m]);
+    // keep every load of the chunk ahead of its first MFMA (the scheduler would otherwise
+    // defer some to save registers)
+    if constexpr (ALL_FIRST) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a[i][u] = ld16_stream(ap[i][u] + k0);
-#pragma unroll
-  for (int j = 0; j < TT; ++j)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) b[j][u] = ld16(bp[j][u] + k0);
-}
-
-template <int RA, int TT>
-__device__ __forceinline__ void wide_mma(u32x4* __restrict__ lds, const u32x4 (&a)[RA][4],
-                                         const u32x4 (&b)[TT][4], f32x4 (&acc)[RA][TT]) {
-  const int l = lane_id(), r = l & 15, q = l >> 4;
-#pragma unroll
-  for (int i = 0; i < RA; ++i)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) lds[(16 * i + 4 * u + q) * 16 + (r ^ (4 * u + q))] = a[i][u];
-#pragma unroll
-  for (int j = 0; j < TT; ++j)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) lds[(16 * (RA + j) + 4 * u + q) * 16 + (r ^ (4 * u + q))] = b[j][u];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int sl = (4 * c + q) ^ r;
-    u32x4 fa[RA], fb[TT];
-#pragma unroll
-    for (int i = 0; i < RA; ++i) fa[i] = lds[(16 * i + r) * 16 + sl];
-#pragma unroll
-    for (int j = 0; j < TT; ++j) fb[j] = lds[(16 * (RA + j) + r) * 16 + sl];
-#pragma unroll
-    for (int i = 0; i < RA; ++i)
-#pragma unroll
-      for (int j = 0; j < TT; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(fa[i]), as_bf16x8(fb[j]),
-                                                            acc[i][j], 0, 0, 0);
+    for (int m = 0; m < MAXB; ++m) split_mma<TT>(slot, a[m], b[m], acc);
   }
 }
 
-// acc += A . B^T over NKB k-blocks, kPD blocks of loads in flight (NKB = 0: rolled loop over K
-// with one block of lookahead). ap/bp are this lane's row pointers, already offset by its
-// 16-byte chunk; all must be valid (padding rows point at real rows, their outputs unused).
-template <int RA, int TT, int NKB>
-__device__ __forceinline__ void wide_dot(u32x4* __restrict__ lds, const uint16_t* const (&ap)[RA][4],
-                                         const uint16_t* const (&bp)[TT][4], int K,
-                                         f32x4 (&acc)[RA][TT]) {
-  if constexpr (NKB > 0) {
-    u32x4 a[NKB][RA][4], b[NKB][TT][4];
+// Writes this wave's partial sums over its transpose slots' LDS (after every wave is done
+// with its slot) and makes them visible to the workgroup.
+template <int TT>
+__device__ __forceinline__ void split_publish(u32x4* lds, int wv, const f32x4 (&acc)[2][TT]) {
+  __syncthreads();
+  f32x4* part = reinterpret_cast<f32x4*>(lds);
 #pragma unroll
-    for (int p = 0; p < kPD && p < NKB; ++p) wide_load<RA, TT>(ap, bp, p * kKBlock, a[p], b[p]);
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int i = 0; i < NKB; ++i) {
-      if (i + kPD < NKB) wide_load<RA, TT>(ap, bp, (i + kPD) * kKBlock, a[i + kPD], b[i + kPD]);
-      wide_mma<RA, TT>(lds, a[i], b[i], acc);
-    }
-  } else {
-    u32x4 a[RA][4], b[TT][4], an[RA][4], bn[TT][4];
-    wide_load<RA, TT>(ap, bp, 0, a, b);
-    for (int kb = 0; kb < K; kb += kKBlock) {
-      if (kb + kKBlock < K) wide_load<RA, TT>(ap, bp, kb + kKBlock, an, bn);
-      wide_mma<RA, TT>(lds, a, b, acc);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int i = 0; i < RA; ++i) a[i][u] = an[i][u];
-#pragma unroll
-        for (int j = 0; j < TT; ++j) b[j][u] = bn[j][u];
-      }
-    }
-  }
+    for (int j = 0; j < TT; ++j) part[((wv * 2 + i) * TT + j) * 64 + lane_id()] = acc[i][j];
+  __syncthreads();
 }
 
-// Calls f.template operator()<NKB>() with NKB = K/128 when that size is unrolled, else 0.
-template <typename F>
-static hipError_t with_nkb(int K, F&& f) {
-  switch (K / kKBlock) {
-    case 1: return f.template operator()<1>();
-    case 2: return f.template operator()<2>();
-    case 3: return f.template operator()<3>();
-    case 4: return f.template operator()<4>();
-    case 6: return f.template operator()<6>();
-    case 8: return f.template operator()<8>();
-    case 16: return f.template operator()<16>();
-    default: return f.template operator()<0>();
-  }
+// Sum over the W waves, in wave order, of accumulator (tile i, token tile j) of lane l.
+template <int TT>
+__device__ __forceinline__ f32x4 split_sum(const u32x4* lds, int W, int i, int j, int l) {
+  const f32x4* part = reinterpret_cast<const f32x4*>(lds);
+  f32x4 v = part[(i * TT + j) * 64 + l];
+  for (int w = 1; w < W; ++w) v += part[((w * 2 + i) * TT + j) * 64 + l];
+  return v;
+}
+
+// Waves and k-blocks per chunk for an item of K/128 k-blocks. Measured on the decode shapes:
+// - two k-blocks per chunk pay off only while the workgroup keeps at least 3 waves (K = 512:
+//   4 waves x 1 beats 2 waves x 2 by 8%);
+// - gate_up with two token tiles runs 27% faster on single-block chunks, its operands for two
+//   blocks would not fit next to each other without halving occupancy;
+// - four token tiles always take single-block chunks.
+// W = the largest divisor of the chunk count up to 8, so every wave gets the same k-blocks.
+struct SplitPlan {
+  int waves, maxb;
+};
+static SplitPlan split_plan(int K, int TT, bool down) {
+  const int nkb = K / kKBlock;
+  auto waves_for = [](int chunks) {
+    int w = kSplitMaxWaves;
+    while (chunks % w != 0) --w;
+    return w;
+  };
+  const bool pairs = nkb % 2 == 0 && (TT == 1 || (TT == 2 && down));
+  if (pairs && waves_for(nkb / 2) >= 3) return {waves_for(nkb / 2), 2};
+  return {waves_for(nkb), 1};
 }
 
 // ---- residual add + RMSNorm ahead of the block (qwen3_5.py:998-1002, :39-55) ---------------
@@ -441,18 +385,25 @@ static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
   return 4;
 }
 
+// Calls f.template operator()<TT, MAXB>() for the plan's MAXB (split_plan gives MAXB = 2 only
+// for one or two token tiles).
+template <int TT, typename F>
+static hipError_t with_maxb(const SplitPlan& plan, F&& f) {
+  if constexpr (TT <= 2) {
+    if (plan.maxb == 2) return f.template operator()<TT, 2>();
+  }
+  return f.template operator()<TT, 1>();
+}
+
 // ---- gate_up + SiLU*mul ------------------------------------------------------------------
-// Wave (channel block cb, group g): gate rows [16cb, 16cb+16) and the matching up rows of
+// Workgroup (channel block cb, group g): gate rows [16cb, 16cb+16) and the matching up rows of
 // expert g; act[row, 16cb + c] = bf16(silu(gate) * up) (chunk(2,-1) + silu*mul of
 // qwen3_5.py:835-836).
-template <int TT, int NKB>
-__global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
-                                                          const uint16_t* __restrict__ x,
-                                                          const int32_t* __restrict__ counts,
-                                                          const int32_t* __restrict__ offsets,
-                                                          const int32_t* __restrict__ perm_tok,
-                                                          int T, int act_ld,
-                                                          uint16_t* __restrict__ act) {
+template <int TT, int MAXB>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T, int act_ld,
+    uint16_t* __restrict__ act) {
   const int g = gw.g0 + blockIdx.y;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
@@ -462,24 +413,23 @@ __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
   if (n == 0) return;
   const int row0 = shared ? gw.sh_row0 : offsets[g];
   const int H = gw.H;
+  const int W = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int per = H / kKBlock / W;
   const int lane = lane_id(), r = lane & 15, q = lane >> 4;
-  const uint16_t* wgt;
-  const uint16_t* wup;
+  const char* wgt;
+  const char* wup;
   if (shared) {
-    wgt = static_cast<const uint16_t*>(gw.sh_gate);
-    wup = static_cast<const uint16_t*>(gw.sh_up);
+    wgt = static_cast<const char*>(gw.sh_gate);
+    wup = static_cast<const char*>(gw.sh_up);
   } else {
-    wgt = static_cast<const uint16_t*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H;
-    wup = wgt + static_cast<int64_t>(gw.I) * H;
+    wgt = static_cast<const char*>(gw.gate_up) + static_cast<int64_t>(g) * 2 * gw.I * H * 2;
+    wup = wgt + static_cast<int64_t>(gw.I) * H * 2;
   }
-  __shared__ u32x4 lds[(2 + TT) * 256];
-  // wide-load row pointers: instruction u covers rows 4u .. 4u+3 of each 16-row tile
-  const uint16_t* ap[2][4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    ap[0][u] = wgt + static_cast<int64_t>(c0 + 4 * u + q) * H + 8 * r;
-    ap[1][u] = wup + static_cast<int64_t>(c0 + 4 * u + q) * H + 8 * r;
-  }
+  const char* abase[2] = {wgt + static_cast<int64_t>(c0) * H * 2,
+                          wup + static_cast<int64_t>(c0) * H * 2};
+  const uint32_t aoff = static_cast<uint32_t>((q * H + 8 * r) * 2);
+  __shared__ u32x4 lds[split_lds_u4<TT>()];
   for (int p0 = 0; p0 < n; p0 += 16 * TT) {
     const uint16_t* bp[TT][4];
 #pragma unroll
@@ -491,56 +441,54 @@ __global__ __launch_bounds__(64) void gate_up_bf16_kernel(GroupWeights gw,
         bp[j][u] = x + static_cast<int64_t>(tok) * H + 8 * r;
       }
     f32x4 acc[2][TT];
-    zero_acc(acc);
-    wide_dot<2, TT, NKB>(lds, ap, bp, H, acc);
-#pragma unroll
-    for (int j = 0; j < TT; ++j) {
+    split_dot<TT, MAXB, false>(lds + wv * 256, abase, 4 * H * 2, aoff, bp, wv * per, per, acc);
+    split_publish<TT>(lds, wv, acc);
+    for (int t = threadIdx.x; t < 64 * TT; t += blockDim.x) {   // (token tile j, lane)
+      const int j = t >> 6;
       const int p = p0 + 16 * j + r;
-      if (p >= n) continue;
-      float a[4];
+      const f32x4 gs = split_sum<TT>(lds, W, 0, j, lane);
+      const f32x4 us = split_sum<TT>(lds, W, 1, j, lane);
+      if (p < n) {
+        float a[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) a[v] = silu(acc[0][j][v]) * acc[1][j][v];
-      u32x2 pk = {pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
-      *reinterpret_cast<u32x2*>(act + static_cast<int64_t>(row0 + p) * act_ld + c0 + 4 * q) = pk;
+        for (int v = 0; v < 4; ++v) a[v] = silu(gs[v]) * us[v];
+        u32x2 pk = {pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+        *reinterpret_cast<u32x2*>(act + static_cast<int64_t>(row0 + p) * act_ld + c0 + 4 * q) = pk;
+      }
     }
+    __syncthreads();   // partial sums read before the next pass reuses the slots
   }
-}
-
-template <int TT>
-static hipError_t launch_gate_up_tt(const GroupWeights& gw, const void* x, const int32_t* counts,
-                                    const int32_t* offsets, const int32_t* perm_tok, int64_t T,
-                                    int act_ld, void* act, hipStream_t s) {
-  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const dim3 grid(Imax / 16, gw.groups);
-  return with_nkb(gw.H, [&]<int NKB>() {
-    gate_up_bf16_kernel<TT, NKB><<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(x), counts,
-                                                     offsets, perm_tok, static_cast<int>(T),
-                                                     act_ld, static_cast<uint16_t*>(act));
-    return hipGetLastError();
-  });
 }
 
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
                                int k, int act_ld, void* act, hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const dim3 grid(Imax / 16, gw.groups);
+  auto go = [&]<int TT>() {
+    const SplitPlan plan = split_plan(gw.H, TT, false);
+    return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
+      gate_up_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
+          gw, static_cast<const uint16_t*>(x), counts, offsets, perm_tok, static_cast<int>(T),
+          act_ld, static_cast<uint16_t*>(act));
+      return hipGetLastError();
+    });
+  };
   switch (pick_tt(gw, T, k)) {
-    case 1: return launch_gate_up_tt<1>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
-    case 2: return launch_gate_up_tt<2>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
-    default: return launch_gate_up_tt<4>(gw, x, counts, offsets, perm_tok, T, act_ld, act, s);
+    case 1: return go.template operator()<1>();
+    case 2: return go.template operator()<2>();
+    default: return go.template operator()<4>();
   }
 }
 
 // ---- down projection ---------------------------------------------------------------------
-// Wave (row block hb, group g): output columns [32hb, 32hb+32) of H for every token row of the
-// group: out[row, h] = bf16(act[row, :Ig] . Wd_g[h, :Ig]) (qwen3_5.py:837, :868, :917).
-template <int TT, int NKB>
-__global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
-                                                       const uint16_t* __restrict__ act,
-                                                       int act_ld,
-                                                       const int32_t* __restrict__ counts,
-                                                       const int32_t* __restrict__ offsets,
-                                                       int T, int width,
-                                                       uint16_t* __restrict__ out) {
+// Workgroup (row block hb, group g): output columns [32hb, 32hb+32) of H for every token row of
+// the group: out[row, h] = bf16(act[row, :Ig] . Wd_g[h, :Ig]) (qwen3_5.py:837, :868, :917).
+template <int TT, int MAXB>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ act, int act_ld,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T, int width,
+    uint16_t* __restrict__ out) {
   const int g = gw.g0 + blockIdx.y;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
@@ -550,17 +498,16 @@ __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
   const int row0 = shared ? gw.sh_row0 : offsets[g];
   const int H = gw.H;
   const int h0 = blockIdx.x * 32;
+  const int W = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int per = Ig / kKBlock / W;
   const int lane = lane_id(), r = lane & 15, q = lane >> 4;
-  const uint16_t* wd = shared ? static_cast<const uint16_t*>(gw.sh_down)
-                              : static_cast<const uint16_t*>(gw.down) +
-                                    static_cast<int64_t>(g) * H * gw.I;
-  __shared__ u32x4 lds[(2 + TT) * 256];
-  const uint16_t* ap[2][4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    ap[0][u] = wd + static_cast<int64_t>(h0 + 4 * u + q) * Ig + 8 * r;
-    ap[1][u] = wd + static_cast<int64_t>(h0 + 16 + 4 * u + q) * Ig + 8 * r;
-  }
+  const char* wd = shared ? static_cast<const char*>(gw.sh_down)
+                          : static_cast<const char*>(gw.down) + static_cast<int64_t>(g) * H * gw.I * 2;
+  const char* abase[2] = {wd + static_cast<int64_t>(h0) * Ig * 2,
+                          wd + static_cast<int64_t>(h0 + 16) * Ig * 2};
+  const uint32_t aoff = static_cast<uint32_t>((q * Ig + 8 * r) * 2);
+  __shared__ u32x4 lds[split_lds_u4<TT>()];
   for (int p0 = 0; p0 < n; p0 += 16 * TT) {
     const uint16_t* bp[TT][4];
 #pragma unroll
@@ -571,53 +518,50 @@ __global__ __launch_bounds__(64) void down_bf16_kernel(GroupWeights gw,
         bp[j][u] = act + static_cast<int64_t>(row0 + p) * act_ld + 8 * r;
       }
     f32x4 acc[2][TT];
-    zero_acc(acc);
-    wide_dot<2, TT, NKB>(lds, ap, bp, Ig, acc);
-#pragma unroll
-    for (int j = 0; j < TT; ++j) {
+    split_dot<TT, MAXB, TT == 2>(lds + wv * 256, abase, 4 * Ig * 2, aoff, bp, wv * per, per, acc);
+    split_publish<TT>(lds, wv, acc);
+    for (int t = threadIdx.x; t < 2 * 64 * TT; t += blockDim.x) {   // (tile i, token tile j, lane)
+      const int i = t >> 6 & 1, j = t >> 7;
       const int p = p0 + 16 * j + r;
-      if (p >= n) continue;
-      uint16_t* orow = out + static_cast<int64_t>(row0 + p) * H + h0 + 4 * q;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        u32x2 pk = {pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3])};
-        *reinterpret_cast<u32x2*>(orow + 16 * i) = pk;
+      const f32x4 v = split_sum<TT>(lds, W, i, j, lane);
+      if (p < n) {
+        u32x2 pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(row0 + p) * H + h0 + 16 * i + 4 * q) = pk;
       }
     }
+    __syncthreads();   // partial sums read before the next pass reuses the slots
   }
 }
 
-template <int TT>
-static hipError_t launch_down_tt(const GroupWeights& gw, const void* act, int act_ld,
-                                 const int32_t* counts, const int32_t* offsets, int64_t T,
-                                 void* out, hipStream_t s) {
+hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
+                            const int32_t* counts, const int32_t* offsets, int64_t T, int k,
+                            void* out, hipStream_t s) {
   const dim3 grid(gw.H / 32, gw.groups);
+  const int tt = pick_tt(gw, T, k);
   auto go = [&](int K) {
-    return with_nkb(K, [&]<int NKB>() {
-      down_bf16_kernel<TT, NKB><<<grid, 64, 0, s>>>(gw, static_cast<const uint16_t*>(act), act_ld,
-                                                    counts, offsets, static_cast<int>(T), K,
-                                                    static_cast<uint16_t*>(out));
-      return hipGetLastError();
-    });
+    auto launch = [&]<int TT>() {
+      const SplitPlan plan = split_plan(K, TT, true);
+      return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
+        down_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
+            gw, static_cast<const uint16_t*>(act), act_ld, counts, offsets, static_cast<int>(T), K,
+            static_cast<uint16_t*>(out));
+        return hipGetLastError();
+      });
+    };
+    switch (tt) {
+      case 1: return launch.template operator()<1>();
+      case 2: return launch.template operator()<2>();
+      default: return launch.template operator()<4>();
+    }
   };
-  // Routed experts (width I) and the shared expert (width Is) each get the kernel unrolled
-  // for their width; a group whose width differs from the launch's exits at once.
+  // Routed experts (width I) and the shared expert (width Is) each get a launch planned for
+  // their width; a group whose width differs from the launch's exits at once.
   const bool has_routed = gw.g0 < gw.E;
   const bool has_shared = gw.g0 + gw.groups > gw.E;
   hipError_t e = hipSuccess;
   if (has_routed) e = go(gw.I);
   if (e == hipSuccess && has_shared && (!has_routed || gw.Is != gw.I)) e = go(gw.Is);
   return e;
-}
-
-hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
-                            const int32_t* counts, const int32_t* offsets, int64_t T, int k,
-                            void* out, hipStream_t s) {
-  switch (pick_tt(gw, T, k)) {
-    case 1: return launch_down_tt<1>(gw, act, act_ld, counts, offsets, T, out, s);
-    case 2: return launch_down_tt<2>(gw, act, act_ld, counts, offsets, T, out, s);
-    default: return launch_down_tt<4>(gw, act, act_ld, counts, offsets, T, out, s);
-  }
 }
 
 }  // namespace lbmoe
