@@ -1,0 +1,74 @@
+// Split-K workgroups of the bf16 weight-streaming decode GEMMs (stream_gemm.hip): the plan and
+// the cross-wave reduction. A workgroup of W waves owns 32 weight rows (two 16-row MFMA tiles)
+// of one group; wave w streams its own k-blocks of those rows and the W partial sums are added
+// in LDS, in wave order. A k-block is 256 bytes of a row, one wide load per 4 rows.
+#pragma once
+#include "common.hpp"
+
+namespace lbmoe {
+
+constexpr int kSplitMaxWaves = 8;
+
+// LDS of a split-K workgroup, in 16-byte units: the waves' transpose slots, later reused for
+// the partial sums [wave][tile i][token tile j][lane].
+template <int TT>
+constexpr int split_lds_u4() {
+  return kSplitMaxWaves * 256 > kSplitMaxWaves * 2 * TT * 64 ? kSplitMaxWaves * 256
+                                                               : kSplitMaxWaves * 2 * TT * 64;
+}
+
+// Writes this wave's partial sums over its transpose slots' LDS (after every wave is done
+// with its slot) and makes them visible to the workgroup.
+template <int TT>
+__device__ __forceinline__ void split_publish(u32x4* lds, int wv, const f32x4 (&acc)[2][TT]) {
+  __syncthreads();
+  f32x4* part = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < TT; ++j) part[((wv * 2 + i) * TT + j) * 64 + lane_id()] = acc[i][j];
+  __syncthreads();
+}
+
+// Sum over the W waves, in wave order, of accumulator (tile i, token tile j) of lane l.
+template <int TT>
+__device__ __forceinline__ f32x4 split_sum(const u32x4* lds, int W, int i, int j, int l) {
+  const f32x4* part = reinterpret_cast<const f32x4*>(lds);
+  f32x4 v = part[(i * TT + j) * 64 + l];
+  for (int w = 1; w < W; ++w) v += part[((w * 2 + i) * TT + j) * 64 + l];
+  return v;
+}
+
+// Waves and k-blocks per chunk for an item of nkb 256-byte k-blocks. Measured on the bf16
+// decode shapes:
+// - two k-blocks per chunk pay off only while the workgroup keeps at least 3 waves (K = 512:
+//   4 waves x 1 beats 2 waves x 2 by 8%);
+// - gate_up with two token tiles runs 27% faster on single-block chunks, its operands for two
+//   blocks would not fit next to each other without halving occupancy;
+// - four token tiles always take single-block chunks.
+// W = the largest divisor of the chunk count up to 8, so every wave gets the same k-blocks.
+struct SplitPlan {
+  int waves, maxb;
+};
+inline SplitPlan split_plan(int nkb, int TT, bool down) {
+  auto waves_for = [](int chunks) {
+    int w = kSplitMaxWaves;
+    while (chunks % w != 0) --w;
+    return w;
+  };
+  const bool pairs = nkb % 2 == 0 && (TT == 1 || (TT == 2 && down));
+  if (pairs && waves_for(nkb / 2) >= 3) return {waves_for(nkb / 2), 2};
+  return {waves_for(nkb), 1};
+}
+
+// Calls f.template operator()<TT, MAXB>() for the plan's MAXB (split_plan gives MAXB = 2 only
+// for one or two token tiles).
+template <int TT, typename F>
+inline hipError_t with_maxb(const SplitPlan& plan, F&& f) {
+  if constexpr (TT <= 2) {
+    if (plan.maxb == 2) return f.template operator()<TT, 2>();
+  }
+  return f.template operator()<TT, 1>();
+}
+
+}  // namespace lbmoe

@@ -25,19 +25,11 @@
 // Accumulator lane (r, q) holds rows 4q..4q+3 of column r.
 #include "common.hpp"
 #include "internal.hpp"
+#include "split_k.hpp"
 
 namespace lbmoe {
 
 constexpr int kKBlock = 128;
-constexpr int kSplitMaxWaves = 8;
-
-// LDS of a split-K workgroup, in 16-byte units: the waves' transpose slots, later reused for
-// the partial sums [wave][tile i][token tile j][lane].
-template <int TT>
-constexpr int split_lds_u4() {
-  return kSplitMaxWaves * 256 > kSplitMaxWaves * 2 * TT * 64 ? kSplitMaxWaves * 256
-                                                               : kSplitMaxWaves * 2 * TT * 64;
-}
 
 // Loads k-block kb of both weight tiles and of the TT token tiles. abase[i] is tile i's
 // wave-uniform base, astep the uniform byte step between load instructions (4 rows) and aoff
@@ -111,50 +103,6 @@ __device__ __forceinline__ void split_dot(u32x4* __restrict__ slot, const char* 
 #pragma unroll
     for (int m = 0; m < MAXB; ++m) split_mma<TT>(slot, a[m], b[m], acc);
   }
-}
-
-// Writes this wave's partial sums over its transpose slots' LDS (after every wave is done
-// with its slot) and makes them visible to the workgroup.
-template <int TT>
-__device__ __forceinline__ void split_publish(u32x4* lds, int wv, const f32x4 (&acc)[2][TT]) {
-  __syncthreads();
-  f32x4* part = reinterpret_cast<f32x4*>(lds);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < TT; ++j) part[((wv * 2 + i) * TT + j) * 64 + lane_id()] = acc[i][j];
-  __syncthreads();
-}
-
-// Sum over the W waves, in wave order, of accumulator (tile i, token tile j) of lane l.
-template <int TT>
-__device__ __forceinline__ f32x4 split_sum(const u32x4* lds, int W, int i, int j, int l) {
-  const f32x4* part = reinterpret_cast<const f32x4*>(lds);
-  f32x4 v = part[(i * TT + j) * 64 + l];
-  for (int w = 1; w < W; ++w) v += part[((w * 2 + i) * TT + j) * 64 + l];
-  return v;
-}
-
-// Waves and k-blocks per chunk for an item of K/128 k-blocks. Measured on the decode shapes:
-// - two k-blocks per chunk pay off only while the workgroup keeps at least 3 waves (K = 512:
-//   4 waves x 1 beats 2 waves x 2 by 8%);
-// - gate_up with two token tiles runs 27% faster on single-block chunks, its operands for two
-//   blocks would not fit next to each other without halving occupancy;
-// - four token tiles always take single-block chunks.
-// W = the largest divisor of the chunk count up to 8, so every wave gets the same k-blocks.
-struct SplitPlan {
-  int waves, maxb;
-};
-static SplitPlan split_plan(int K, int TT, bool down) {
-  const int nkb = K / kKBlock;
-  auto waves_for = [](int chunks) {
-    int w = kSplitMaxWaves;
-    while (chunks % w != 0) --w;
-    return w;
-  };
-  const bool pairs = nkb % 2 == 0 && (TT == 1 || (TT == 2 && down));
-  if (pairs && waves_for(nkb / 2) >= 3) return {waves_for(nkb / 2), 2};
-  return {waves_for(nkb), 1};
 }
 
 // ---- residual add + RMSNorm ahead of the block (qwen3_5.py:998-1002, :39-55) ---------------
@@ -385,16 +333,6 @@ static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
   return 4;
 }
 
-// Calls f.template operator()<TT, MAXB>() for the plan's MAXB (split_plan gives MAXB = 2 only
-// for one or two token tiles).
-template <int TT, typename F>
-static hipError_t with_maxb(const SplitPlan& plan, F&& f) {
-  if constexpr (TT <= 2) {
-    if (plan.maxb == 2) return f.template operator()<TT, 2>();
-  }
-  return f.template operator()<TT, 1>();
-}
-
 // ---- gate_up + SiLU*mul ------------------------------------------------------------------
 // Workgroup (channel block cb, group g): gate rows [16cb, 16cb+16) and the matching up rows of
 // expert g; act[row, 16cb + c] = bf16(silu(gate) * up) (chunk(2,-1) + silu*mul of
@@ -466,7 +404,7 @@ hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int3
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   const dim3 grid(Imax / 16, gw.groups);
   auto go = [&]<int TT>() {
-    const SplitPlan plan = split_plan(gw.H, TT, false);
+    const SplitPlan plan = split_plan(gw.H / kKBlock, TT, false);
     return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
       gate_up_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
           gw, static_cast<const uint16_t*>(x), counts, offsets, perm_tok, static_cast<int>(T),
@@ -540,7 +478,7 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
   const int tt = pick_tt(gw, T, k);
   auto go = [&](int K) {
     auto launch = [&]<int TT>() {
-      const SplitPlan plan = split_plan(K, TT, true);
+      const SplitPlan plan = split_plan(K / kKBlock, TT, true);
       return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
         down_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
             gw, static_cast<const uint16_t*>(act), act_ld, counts, offsets, static_cast<int>(T), K,
