@@ -178,9 +178,8 @@ def pmc_traffic(kernel):
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                parts = line.split()
-                if len(parts) == 4 and parts[0] == kernel:
-                    return int(parts[3])
+                if line.startswith(kernel) and line[len(kernel)] in " <":
+                    return int(line.split()[-1])
     except OSError:
         pass
     return None

@@ -308,6 +308,13 @@ hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E,
                                      logits, s);
 }
 
+// Token count up to which the norm runs inside the router. Every expert tile's workgroup
+// recomputes its tokens' norm and cannot start its MFMAs before the whole row is summed, so
+// the fused kernel loses to add_rmsnorm_kernel + the plain router as T grows (Qwen3-30B-A3B
+// layer, back-to-back calls: T=1 41.5 vs 42.7 us, T=32 185.4 vs 184.4, T=128 227.0 vs 224.6,
+// T=512 431 vs 422).
+constexpr int64_t kNormFusedMaxTokens = 16;
+
 hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, const void* norm_w,
                                      float eps, const void* wg, int64_t T, int E, int H,
                                      void* logits, void* x_out, void* res_out, hipStream_t s) {
@@ -315,7 +322,7 @@ hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, c
                   static_cast<const uint16_t*>(norm_w), eps, static_cast<uint16_t*>(x_out),
                   static_cast<uint16_t*>(res_out)};
   const int per_wave = (H / kKBlock + kRouterWaves - 1) / kRouterWaves;
-  if (T < kTiledRouterMinTokens && per_wave <= kRouterNormBlocks)
+  if (T <= kNormFusedMaxTokens && per_wave <= kRouterNormBlocks)
     return launch_router_decode<true>(nullptr, nm, wg, T, E, H, logits, s);
   add_rmsnorm_kernel<<<static_cast<unsigned>((T + 3) / 4), 256, 0, s>>>(
       nm.hidden, nm.residual, nm.weight, eps, static_cast<int>(T), H, nm.x_out, nm.res_out);

@@ -74,18 +74,21 @@ def test_decode_bucket_graphs(gpu):
     """The engine's decode capture (model_runner.py:1463-1507): one graph per batch bucket,
     captured from the largest bucket down in a shared memory pool, all reading slices of one
     static input buffer whose rows past the live batch are zeros (padded rows are routed like
-    real ones). Every bucket's replay matches an eager call on the same slice bit for bit."""
+    real ones), and one workspace for all of them. Every bucket's replay matches an eager call
+    on the same slice bit for bit."""
     buckets = [1, 2, 4, 8, 16, 32, 48, 64]
     w, g = make_layer(SHAPE, seed=11)
     blk = _block(SHAPE, {k: v.to(gpu) for k, v in w.items()}, gpu)
     static_x = torch.zeros((max(buckets), SHAPE.hidden_size), dtype=torch.bfloat16, device=gpu)
     outputs = torch.zeros_like(static_x)
+    # one workspace, sized for the largest bucket, shared by every graph
+    ws = torch.empty(blk.workspace_size(max(buckets)), dtype=torch.uint8, device=gpu)
     graphs, pool = {}, None
     for bs in reversed(buckets):
-        outputs[:bs] = blk(static_x[:bs])                        # warm-up
+        outputs[:bs] = blk(static_x[:bs], workspace=ws)          # warm-up
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool):
-            outputs[:bs] = blk(static_x[:bs])
+            outputs[:bs] = blk(static_x[:bs], workspace=ws)
         if pool is None:
             pool = graph.pool()
         graphs[bs] = graph

@@ -250,8 +250,10 @@ class _Norm(torch.nn.Module):
         self.eps = eps
 
 
+# T <= 16 runs the norm inside the router kernel, larger T as its own kernel ahead of the router
 @pytest.mark.parametrize("shape_name,T", [("small-h1024-e16", 40), ("qwen3-30b-a3b", 128),
-                                          ("qwen3-30b-a3b", 1), ("qwen3-next-e512", 1100)])
+                                          ("qwen3-30b-a3b", 1), ("qwen3-30b-a3b", 16),
+                                          ("small-h1024-e16", 13), ("qwen3-next-e512", 1100)])
 def test_forward_norm(gpu, shape_name, T):
     """Residual add + RMSNorm + block (qwen3_5.py:998-1004): the new residual is the bf16 sum
     bit for bit, the block input within one bf16 step of the oracle's Qwen3_5RMSNorm, and the
