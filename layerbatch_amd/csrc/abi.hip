@@ -152,7 +152,11 @@ static P* at(void* ws, const WsLayout& w, int r) {
   } while (0)
 
 // Expected tokens per routed expert at which the LDS-tiled GEMMs replace weight streaming.
-constexpr double kTiledMinTokensPerExpert = 48.0;
+// Measured (back-to-back µs per layer call): at 24 tokens per expert both are even
+// (Qwen3-30B-A3B T=384: 286-291); from 30 on the tiled GEMMs win clearly (T=512: 293 vs 431,
+// E=512 T=1536: 731 vs 998), the streaming kernels then needing four token tiles per pass;
+// at 20 streaming wins (E=512 T=1024: 672 vs 714, fp8 427 vs 484).
+constexpr double kTiledMinTokensPerExpert = 28.0;
 
 static bool use_tiled(const GroupWeights& gw, int64_t T, int k) {
   return tiled_supported(gw) && static_cast<double>(T) * k / gw.E >= kTiledMinTokensPerExpert;

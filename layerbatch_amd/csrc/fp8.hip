@@ -205,9 +205,11 @@ __global__ __launch_bounds__(64) void gate_up_fp8_kernel(GroupWeights gw, const 
                                                          const int32_t* __restrict__ counts,
                                                          const int32_t* __restrict__ offsets,
                                                          const int32_t* __restrict__ perm_tok,
-                                                         int T, int act_ld, uint16_t* __restrict__ act) {
+                                                         int T, int shared_extra, int act_ld,
+                                                         uint16_t* __restrict__ act) {
   __shared__ u32x4 lds[(2 + TT) * 256];
-  const int g = gw.g0 + blockIdx.y;
+  const GroupSlice gs = group_slice(gw, shared_extra);
+  const int g = gs.g;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(64) void gate_up_fp8_kernel(GroupWeights gw, const 
     ap[1][u] = wup + static_cast<int64_t>(c0 + 4 * u + q) * H + 16 * r;
   }
   const float* wsp[2] = {sg, su};
-  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
     const uint8_t* bp[TT][4];
     const float* xsp[TT];
 #pragma unroll
@@ -277,9 +279,10 @@ __global__ __launch_bounds__(64) void down_fp8_kernel(GroupWeights gw, const uin
                                                       const float* __restrict__ as, int act_ld,
                                                       const int32_t* __restrict__ counts,
                                                       const int32_t* __restrict__ offsets, int T,
-                                                      uint16_t* __restrict__ out) {
+                                                      int shared_extra, uint16_t* __restrict__ out) {
   __shared__ u32x4 lds[(2 + TT) * 256];
-  const int g = gw.g0 + blockIdx.y;
+  const GroupSlice gs = group_slice(gw, shared_extra);
+  const int g = gs.g;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int n = shared ? T : counts[g];
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(64) void down_fp8_kernel(GroupWeights gw, const uin
     ap[1][u] = wd + static_cast<int64_t>(h0 + 16 + 4 * u + q) * Ig + 16 * r;
   }
   const float* wsp[2] = {sd, sd};
-  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
     const uint8_t* bp[TT][4];
     const float* xsp[TT];
 #pragma unroll
@@ -338,36 +341,40 @@ static int pick_tt8(const GroupWeights& gw, int64_t T, int k) {
   return avg <= 12.0 ? 1 : (avg <= 28.0 ? 2 : 4);
 }
 
+// Calls f.template operator()<TT>() for the token-tile count tt.
+template <typename F>
+static hipError_t with_tt8(int tt, F&& f) {
+  switch (tt) {
+    case 1: return f.template operator()<1>();
+    case 2: return f.template operator()<2>();
+    default: return f.template operator()<4>();
+  }
+}
+
 hipError_t launch_gate_up_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                               const int32_t* counts, const int32_t* offsets,
                               const int32_t* perm_tok, int64_t T, int k, int act_ld, void* act,
                               hipStream_t s) {
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const dim3 grid(Imax / 16, gw.groups);
-  const auto* x8 = static_cast<const uint8_t*>(xq);
-  auto* a = static_cast<uint16_t*>(act);
-  const int Ti = static_cast<int>(T);
-  switch (pick_tt8(gw, T, k)) {
-    case 1: gate_up_fp8_kernel<1><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
-    case 2: gate_up_fp8_kernel<2><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
-    default: gate_up_fp8_kernel<4><<<grid, 64, 0, s>>>(gw, x8, xs, counts, offsets, perm_tok, Ti, act_ld, a); break;
-  }
-  return hipGetLastError();
+  return with_tt8(pick_tt8(gw, T, k), [&]<int TT>() {
+    const int extra = shared_extra_rows(gw, T, 16 * TT);
+    gate_up_fp8_kernel<TT><<<dim3(Imax / 16, gw.groups + extra), 64, 0, s>>>(
+        gw, static_cast<const uint8_t*>(xq), xs, counts, offsets, perm_tok, static_cast<int>(T),
+        extra, act_ld, static_cast<uint16_t*>(act));
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_down_fp8(const GroupWeights& gw, const void* actq, const float* acts,
                            int act_ld, const int32_t* counts, const int32_t* offsets,
                            int64_t T, int k, void* out, hipStream_t s) {
-  const dim3 grid(gw.H / 32, gw.groups);
-  const auto* a8 = static_cast<const uint8_t*>(actq);
-  auto* o = static_cast<uint16_t*>(out);
-  const int Ti = static_cast<int>(T);
-  switch (pick_tt8(gw, T, k)) {
-    case 1: down_fp8_kernel<1><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
-    case 2: down_fp8_kernel<2><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
-    default: down_fp8_kernel<4><<<grid, 64, 0, s>>>(gw, a8, acts, act_ld, counts, offsets, Ti, o); break;
-  }
-  return hipGetLastError();
+  return with_tt8(pick_tt8(gw, T, k), [&]<int TT>() {
+    const int extra = shared_extra_rows(gw, T, 16 * TT);
+    down_fp8_kernel<TT><<<dim3(gw.H / 32, gw.groups + extra), 64, 0, s>>>(
+        gw, static_cast<const uint8_t*>(actq), acts, act_ld, counts, offsets,
+        static_cast<int>(T), extra, static_cast<uint16_t*>(out));
+    return hipGetLastError();
+  });
 }
 
 }  // namespace lbmoe

@@ -56,6 +56,29 @@ struct GroupWeights {
   int sh_row0;
 };
 
+// Grids of the weight-streaming GEMMs: row y < groups of workgroups serves group g0 + y. The
+// shared expert (the last group, when the launch has it) takes all T tokens, which one
+// workgroup would walk pass after pass; it gets shared_extra more rows of workgroups, and
+// slice s of its nslices takes passes s, s + nslices, ...
+struct GroupSlice {
+  int g, slice, nslices;
+};
+__device__ __forceinline__ GroupSlice group_slice(const GroupWeights& gw, int shared_extra) {
+  const int y = blockIdx.y;
+  if (y < gw.groups) {
+    const int g = gw.g0 + y;
+    return {g, 0, g == gw.E ? shared_extra + 1 : 1};
+  }
+  return {gw.E, y - gw.groups + 1, shared_extra + 1};
+}
+constexpr int kMaxSharedSlices = 16;
+// Extra workgroup rows for the shared expert at tokens_per_pass tokens per pass.
+inline int shared_extra_rows(const GroupWeights& gw, int64_t T, int tokens_per_pass) {
+  if (gw.g0 + gw.groups <= gw.E) return 0;
+  const int64_t passes = (T + tokens_per_pass - 1) / tokens_per_pass;
+  return static_cast<int>((passes < kMaxSharedSlices ? passes : kMaxSharedSlices) - (passes > 0));
+}
+
 // ---- launchers (each returns hipError_t of the launch) ----------------------------------
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
                                 void* logits, hipStream_t s);

@@ -347,9 +347,10 @@ static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
 template <int TT, int MAXB>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
     GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T, int act_ld,
-    uint16_t* __restrict__ act) {
-  const int g = gw.g0 + blockIdx.y;
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T,
+    int shared_extra, int act_ld, uint16_t* __restrict__ act) {
+  const GroupSlice gs = group_slice(gw, shared_extra);
+  const int g = gs.g;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
                           wup + static_cast<int64_t>(c0) * H * 2};
   const uint32_t aoff = static_cast<uint32_t>((q * H + 8 * r) * 2);
   __shared__ u32x4 lds[split_lds_u4<TT>()];
-  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
     const uint16_t* bp[TT][4];
 #pragma unroll
     for (int j = 0; j < TT; ++j)
@@ -409,13 +410,14 @@ hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int3
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
                                int k, int act_ld, void* act, hipStream_t s) {
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  const dim3 grid(Imax / 16, gw.groups);
   auto go = [&]<int TT>() {
+    const int extra = shared_extra_rows(gw, T, 16 * TT);
+    const dim3 grid(Imax / 16, gw.groups + extra);
     const SplitPlan plan = split_plan(gw.H / kKBlock, TT, false);
     return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
       gate_up_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
           gw, static_cast<const uint16_t*>(x), counts, offsets, perm_tok, static_cast<int>(T),
-          act_ld, static_cast<uint16_t*>(act));
+          extra, act_ld, static_cast<uint16_t*>(act));
       return hipGetLastError();
     });
   };
@@ -432,9 +434,10 @@ hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int3
 template <int TT, int MAXB>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
     GroupWeights gw, const uint16_t* __restrict__ act, int act_ld,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T, int width,
-    uint16_t* __restrict__ out) {
-  const int g = gw.g0 + blockIdx.y;
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T,
+    int shared_extra, int width, uint16_t* __restrict__ out) {
+  const GroupSlice gs = group_slice(gw, shared_extra);
+  const int g = gs.g;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   if (Ig != width) return;          // groups of another width run in their own launch
@@ -453,7 +456,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
                           wd + static_cast<int64_t>(h0 + 16) * Ig * 2};
   const uint32_t aoff = static_cast<uint32_t>((q * Ig + 8 * r) * 2);
   __shared__ u32x4 lds[split_lds_u4<TT>()];
-  for (int p0 = 0; p0 < n; p0 += 16 * TT) {
+  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
     const uint16_t* bp[TT][4];
 #pragma unroll
     for (int j = 0; j < TT; ++j)
@@ -481,15 +484,16 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
                             const int32_t* counts, const int32_t* offsets, int64_t T, int k,
                             void* out, hipStream_t s) {
-  const dim3 grid(gw.H / 32, gw.groups);
   const int tt = pick_tt(gw, T, k);
   auto go = [&](int K) {
     auto launch = [&]<int TT>() {
+      const int extra = shared_extra_rows(gw, T, 16 * TT);
+      const dim3 grid(gw.H / 32, gw.groups + extra);
       const SplitPlan plan = split_plan(K / kKBlock, TT, true);
       return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
         down_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
-            gw, static_cast<const uint16_t*>(act), act_ld, counts, offsets, static_cast<int>(T), K,
-            static_cast<uint16_t*>(out));
+            gw, static_cast<const uint16_t*>(act), act_ld, counts, offsets, static_cast<int>(T),
+            extra, K, static_cast<uint16_t*>(out));
         return hipGetLastError();
       });
     };
