@@ -84,6 +84,12 @@ def test_fp8_block_small(gpu, T):
     _run_fp8(MoEShape(1024, 16, 2, 512, 0), T, gpu, seed=T)
 
 
+# E not a multiple of 16, odd k, H with 6 k-blocks of 256 bytes, I = 3 such blocks
+@pytest.mark.parametrize("T", [37, 300])
+def test_fp8_block_odd_shape(gpu, T):
+    _run_fp8(MoEShape(1536, 20, 3, 768, 256), T, gpu, seed=T)
+
+
 def test_fp8_block_shared(gpu):
     _run_fp8(MoEShape(1024, 32, 4, 256, 512), 96, gpu, seed=5)
 

@@ -89,6 +89,21 @@ def test_block_with_shared_expert(gpu):
     _run_and_check(shape, 40, gpu, seed=3)
 
 
+# Shapes off the benchmark grid: E not a multiple of the 16-expert router tile, odd k, H with
+# 12 and 32 k-blocks (split-K plans of 6 waves, and of 8 waves x 2 chunks each), widths of 3
+# and 5 k-blocks, Is != I; streaming (small T) and LDS-tiled (large T) GEMMs, and H = 640, which
+# the tiled GEMMs do not take, streaming 50 tokens per expert (four token tiles per pass).
+@pytest.mark.parametrize("shape,T", [(MoEShape(1536, 20, 3, 384, 640), 1),
+                                     (MoEShape(1536, 20, 3, 384, 640), 37),
+                                     (MoEShape(1536, 20, 3, 384, 640), 260),
+                                     (MoEShape(4096, 24, 4, 256, 0), 5),
+                                     (MoEShape(4096, 24, 4, 256, 0), 60),
+                                     (MoEShape(640, 40, 5, 128, 128), 90),
+                                     (MoEShape(640, 40, 5, 128, 128), 400)])
+def test_block_odd_shapes(gpu, shape, T):
+    _run_and_check(shape, T, gpu, seed=T + shape.num_experts)
+
+
 def test_block_with_bias(gpu):
     shape = MoEShape(1024, 64, 6, 256, 0)
     g = torch.Generator().manual_seed(11)
