@@ -13,7 +13,8 @@
 //   offsets   one workgroup: exclusive scan of the totals -> counts[e], offsets[e].
 //   scatter   one wave per chunk: pos = offsets[e] + base[e][chunk] + rank -> perm_tok,
 //             perm_slot, inv.
-// Up to kPermSingle entries (decode-sized batches) run all of it in a single workgroup.
+// Up to 2 * kPermSingle entries (4 * kPermSingle for E <= 512), i.e. decode-sized batches, run
+// all of it in a single workgroup.
 // Entries whose expert id lies outside [0, E) are left out of every list and get inv = -1.
 #include "common.hpp"
 #include "internal.hpp"
@@ -177,39 +178,53 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
   }
 }
 
-// Whole permutation in one workgroup when V <= kPermSingle (decode-sized batches): wave w
-// takes entries v = 64w .. 64w+63, ranks them among equal experts of the wave (ballot match),
-// and records the wave's count per expert; one thread per expert then turns the counts into
-// per-wave prefixes and a total, a block scan of the totals gives the offsets, and every
-// entry lands at offsets[e] + (entries of e in earlier waves) + rank.
-template <int IB>
+// Whole permutation in one workgroup for decode-sized batches (V <= R * kPermSingle): thread
+// tid takes entries v = r * kPermSingle + tid, r < R, so that "virtual wave" vw = v / 64 =
+// r * (kPermSingle / 64) + wave covers 64 consecutive entries. Each virtual wave ranks its
+// entries among equal experts (ballot match) and records its count per expert; one thread per
+// expert then turns the counts into per-virtual-wave prefixes (in v order) and a total, a block
+// scan of the totals gives the offsets, and every entry lands at offsets[e] + (entries of e in
+// earlier virtual waves) + rank.
+template <int IB, int R, int EMAX>
 __global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int T, int k, int E,
                                                            int nbits, int V, int32_t* counts,
                                                            int32_t* offsets, int32_t* perm_tok,
                                                            int32_t* perm_slot, int32_t* inv) {
   constexpr int kW = kPermSingle / kWave;
-  __shared__ int cnt[kW][1024];          // per wave and expert: count, then exclusive prefix
-  __shared__ int start[1024];
+  constexpr int kVW = kW * R;            // virtual waves
+  __shared__ int cnt[kVW][EMAX];         // per virtual wave and expert: count, then prefix
+  __shared__ int start[EMAX];
   __shared__ int wsum[kW];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  for (int i = tid; i < kW * 1024; i += kPermSingle) (&cnt[0][0])[i] = 0;
-  const int v = tid;
-  int e = -1, s = 0, t = 0;
-  if (v < V) {
-    s = v / T;
-    t = v - s * T;
-    e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
+  for (int i = tid; i < kVW * EMAX; i += kPermSingle) (&cnt[0][0])[i] = 0;
+  int e[R], s[R], t[R], rank[R];
+  bool valid[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int v = r * kPermSingle + tid;
+    e[r] = -1;
+    s[r] = t[r] = 0;
+    if (v < V) {
+      s[r] = v / T;
+      t[r] = v - s[r] * T;
+      e[r] = load_expert<IB>(idx, static_cast<int64_t>(t[r]) * k + s[r]);
+    }
   }
-  const bool valid = (e >= 0) && (e < E);
-  const uint64_t m = match_expert(valid ? e : 0, __ballot(valid), nbits);
-  const int rank = mask_rank(m);
+  uint64_t m[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    valid[r] = (e[r] >= 0) && (e[r] < E);
+    m[r] = match_expert(valid[r] ? e[r] : 0, __ballot(valid[r]), nbits);
+    rank[r] = mask_rank(m[r]);
+  }
   __syncthreads();
-  if (valid && rank == 0) cnt[wave][e] = __popcll(m);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (valid[r] && rank[r] == 0) cnt[r * kW + wave][e[r]] = __popcll(m[r]);
   __syncthreads();
   int total = 0;
   if (tid < E) {
-#pragma unroll
-    for (int w = 0; w < kW; ++w) {
+    for (int w = 0; w < kVW; ++w) {
       const int c = cnt[w][tid];
       cnt[w][tid] = total;
       total += c;
@@ -233,14 +248,16 @@ __global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int 
   }
   if (tid == kPermSingle - 1) offsets[E] = before + incl;
   __syncthreads();
-  if (v < V) {
-    const int64_t ts = static_cast<int64_t>(t) * k + s;
-    if (!valid) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r * kPermSingle + tid >= V) continue;
+    const int64_t ts = static_cast<int64_t>(t[r]) * k + s[r];
+    if (!valid[r]) {
       inv[ts] = -1;
     } else {
-      const int pos = start[e] + cnt[wave][e] + rank;
-      perm_tok[pos] = t;
-      perm_slot[pos] = s;
+      const int pos = start[e[r]] + cnt[r * kW + wave][e[r]] + rank[r];
+      perm_tok[pos] = t[r];
+      perm_slot[pos] = s[r];
       inv[ts] = pos;
     }
   }
@@ -270,11 +287,16 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
                                    hipStream_t s) {
   const int V = static_cast<int>(T * k);
   const int nbits = bits_for(E);
-  if (V <= kPermSingle) {
-    perm_single<IB><<<1, kPermSingle, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, counts,
-                                              offsets, perm_tok, perm_slot, inv);
+  // one workgroup up to 2 (4 for E <= 512) entries per thread; the LDS count table is
+  // (16 * R) x EMAX ints, at most 128 KB
+  auto single = [&]<int R, int EMAX>() {
+    perm_single<IB, R, EMAX><<<1, kPermSingle, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V,
+                                                       counts, offsets, perm_tok, perm_slot, inv);
     return hipGetLastError();
-  }
+  };
+  if (V <= kPermSingle) return single.template operator()<1, 1024>();
+  if (V <= 2 * kPermSingle) return single.template operator()<2, 1024>();
+  if (V <= 4 * kPermSingle && E <= 512) return single.template operator()<4, 512>();
   // hist, base: E x nblk; lrank: V; the totals reuse the counts array until perm_offsets
   const int nblk = static_cast<int>(perm_blocks(V));
   perm_count<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist,

@@ -134,7 +134,10 @@ def test_dense_reduction_e1_k1(gpu):
 @pytest.mark.parametrize("T,k,E,ib", [(1, 1, 1, 4), (7, 2, 16, 8), (128, 8, 128, 4),
                                       (129, 8, 128, 8), (1000, 10, 512, 4), (8192, 8, 128, 4),
                                       (3000, 7, 1000, 8), (0, 4, 16, 4), (100, 10, 1024, 8),
-                                      (32, 32, 64, 4)])
+                                      (32, 32, 64, 4),
+                                      # one workgroup, 2 and 4 entries per thread; 4 needs E <= 512
+                                      (256, 8, 128, 4), (200, 10, 1024, 8), (300, 10, 512, 8),
+                                      (409, 10, 512, 4), (250, 10, 1000, 4)])
 def test_permute_exact(gpu, lbmoe, T, k, E, ib):
     rng = np.random.default_rng(T * 131 + k)
     idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]) if T else np.zeros((0, k), np.int64)
