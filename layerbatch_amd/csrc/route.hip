@@ -65,18 +65,40 @@ __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ l
   float z[EPL];
   uint32_t key[EPL];
   float m = -INFINITY;
+  // unconditional loads (lanes past E read expert E-1 and are masked): a load under a
+  // condition would make the compiler wait for it before the next one is issued
+  uint16_t lv[EPL];
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = min(j * kWave + lane, E - 1);
+    lv[j] = lrow[e];
+    bv[j] = bias ? bias[e] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
-    float v = -INFINITY;
-    if (e < E) {
-      v = bf2f(lrow[e]);
-      if (bias) v += bias[e];
-      if (!(v == v)) v = -INFINITY;     // a NaN logit is never preferred
-    }
+    float v = bf2f(lv[j]) + bv[j];
+    if (!(v == v) || e >= E) v = -INFINITY;   // a NaN logit is never preferred
     z[j] = v;
-    key[j] = e < E ? order_key(v) : 0u;   // 0 is below every valid key
+    key[j] = e < E ? order_key(v) : 0u;       // 0 is below every valid key
     m = fmaxf(m, v);
+  }
+  // the shared-expert gate, its loads in flight together with the logits'
+  if (sgate != nullptr) {
+    const uint16_t* xr = x + static_cast<int64_t>(t) * H;
+    float d = 0.f;
+    for (int c = lane * 8; c < H; c += kWave * 8) {
+      const u32x4 a = ld16(xr + c);
+      const u32x4 b = ld16(w_sg + c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        d += bf_lo(a[q]) * bf_lo(b[q]);
+        d += bf_hi(a[q]) * bf_hi(b[q]);
+      }
+    }
+    d = round_bf(wave_sum(d));
+    if (lane == 0) sgate[t] = 1.0f / (1.0f + expf(-d));
   }
   m = wave_max(m);
   float part = 0.f;
@@ -126,21 +148,6 @@ __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ l
     topw[o] = static_cast<uint16_t>(f2bf(p / psum));
     if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o] = my_e;
     else reinterpret_cast<int32_t*>(idx_out)[o] = my_e;
-  }
-  if (sgate != nullptr) {
-    const uint16_t* xr = x + static_cast<int64_t>(t) * H;
-    float d = 0.f;
-    for (int c = lane * 8; c < H; c += kWave * 8) {
-      const u32x4 a = ld16(xr + c);
-      const u32x4 b = ld16(w_sg + c);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        d += bf_lo(a[q]) * bf_lo(b[q]);
-        d += bf_hi(a[q]) * bf_hi(b[q]);
-      }
-    }
-    d = round_bf(wave_sum(d));
-    if (lane == 0) sgate[t] = 1.0f / (1.0f + expf(-d));
   }
 }
 
