@@ -44,17 +44,18 @@ __device__ __forceinline__ void rank_chunk(const void* idx, int T, int k, int E,
                                            int V, int v0, int* run, int (&e_out)[ROUNDS],
                                            int (&rk_out)[ROUNDS]) {
   const int lane = lane_id();
+  // unconditional loads (entries past V read entry V-1 and are masked): a load under a
+  // condition would make the compiler wait for it before issuing the next; V >= 1 here
 #pragma unroll
   for (int r = 0; r < ROUNDS; ++r) {
-    const int v = v0 + r * kWave + lane;
-    int e = -1;
-    if (v < V) {
-      const int s = v / T;
-      const int t = v - s * T;
-      e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
-    }
-    e_out[r] = e;
+    const int v = min(v0 + r * kWave + lane, V - 1);
+    const int s = v / T;
+    const int t = v - s * T;
+    e_out[r] = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
   }
+#pragma unroll
+  for (int r = 0; r < ROUNDS; ++r)
+    if (v0 + r * kWave + lane >= V) e_out[r] = -1;
 #pragma unroll
   for (int r = 0; r < ROUNDS; ++r) {
     const int e = e_out[r];
@@ -160,12 +161,21 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
                                                    int32_t* inv) {
   const int lane = lane_id();
   const int b = blockIdx.x;
+  // every expert id first, unconditionally (entries past V read entry V-1, V >= 1 here)
+  int ev[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int v = min(b * kPermChunk + r * kWave + lane, V - 1);
+    const int s = v / T;
+    ev[r] = load_expert<IB>(idx, static_cast<int64_t>(v - s * T) * k + s);
+  }
+#pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int v = b * kPermChunk + r * kWave + lane;
     if (v >= V) break;
     const int s = v / T;
     const int t = v - s * T;
-    const int e = load_expert<IB>(idx, static_cast<int64_t>(t) * k + s);
+    const int e = ev[r];
     const int64_t ts = static_cast<int64_t>(t) * k + s;
     if (e < 0 || e >= E) {
       inv[ts] = -1;
@@ -199,16 +209,23 @@ __global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int 
   for (int i = tid; i < kVW * EMAX; i += kPermSingle) (&cnt[0][0])[i] = 0;
   int e[R], s[R], t[R], rank[R];
   bool valid[R];
+  // unconditional loads (entries past V read entry V-1 and are masked); V = 0 reads nothing
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int v = r * kPermSingle + tid;
     e[r] = -1;
     s[r] = t[r] = 0;
-    if (v < V) {
+  }
+  if (V > 0) {                           // the same for every thread
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int v = min(r * kPermSingle + tid, V - 1);
       s[r] = v / T;
       t[r] = v - s[r] * T;
       e[r] = load_expert<IB>(idx, static_cast<int64_t>(t[r]) * k + s[r]);
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r * kPermSingle + tid >= V) e[r] = -1;
   }
   uint64_t m[R];
 #pragma unroll
