@@ -90,9 +90,11 @@ hipError_t launch_quant_groups_fp8(const void* a, int64_t rows, int cols, int ld
 }  // namespace lbmoe
 
 // ---- fp8 weight-streaming GEMMs -----------------------------------------------------------
-// Same scheme as the bf16 streaming kernels (stream_gemm.hip): a wave owns 16 weight rows per
-// tile (RA tiles) and streams them once per pass over its group's tokens, loading 4 rows x 256
-// contiguous bytes per instruction and transposing through a per-wave LDS scratch. With one
+// One wave owns 16 weight rows per tile (RA tiles) and streams them once per pass over its
+// group's tokens, loading 4 rows x 256 contiguous bytes per instruction and transposing through
+// a per-wave LDS scratch, as the bf16 decode GEMMs do (stream_gemm.hip) but without their
+// split-K workgroups: an fp8 row block carries half the bytes, and split across waves the
+// per-workgroup overhead outweighed the burst (measured slower). With one
 // byte per element a 256-byte row segment is 256 k; it holds two 128-k scale blocks, each
 // one v_mfma_scale_f32_16x16x128_f8f6f4 (OCP e4m3 operands, unit E8M0 block scales): lane
 // (r, q) supplies 32 bytes k = 128c + 32q .. +32 of row r. The block product is scaled by
