@@ -7,7 +7,11 @@
 
 namespace lbmoe {
 
+// Launch bounds and LDS are sized for kSplitMaxWaves waves; the plans use at most
+// kSplitPlanWaves. (Sizing for 4 made the compiler trade loads in flight for occupancy and ran
+// slower: gate_up at 256 tokens 155 vs 141 us.)
 constexpr int kSplitMaxWaves = 8;
+constexpr int kSplitPlanWaves = 4;
 
 // LDS of a split-K workgroup, in 16-byte units: the waves' transpose slots, later reused for
 // the partial sums [wave][tile i][token tile j][lane].
@@ -45,14 +49,16 @@ __device__ __forceinline__ f32x4 split_sum(const u32x4* lds, int W, int i, int j
 //   4 waves x 1 beats 2 waves x 2 by 8%);
 // - gate_up with two token tiles runs 27% faster on single-block chunks, its operands for two
 //   blocks would not fit next to each other without halving occupancy;
-// - four token tiles always take single-block chunks.
-// W = the largest divisor of the chunk count up to 8, so every wave gets the same k-blocks.
+// - four token tiles always take single-block chunks;
+// - 4 waves per workgroup beat 8 (gate_up at 128 tokens 135.8 -> 127.5 us, E=512 494 -> 476 us
+//   for the layer): each wave then walks two chunks, and four workgroups share a CU.
+// W = the largest divisor of the chunk count up to 4, so every wave gets the same k-blocks.
 struct SplitPlan {
   int waves, maxb;
 };
 inline SplitPlan split_plan(int nkb, int TT, bool down) {
   auto waves_for = [](int chunks) {
-    int w = kSplitMaxWaves;
+    int w = kSplitPlanWaves;
     while (chunks % w != 0) --w;
     return w;
   };
