@@ -45,11 +45,11 @@ __device__ __forceinline__ f32x4 split_sum(const u32x4* lds, int W, int i, int j
 
 // Waves and k-blocks per chunk for an item of nkb 256-byte k-blocks. Measured on the bf16
 // decode shapes:
-// - two k-blocks per chunk pay off only while the workgroup keeps at least 3 waves (K = 512:
-//   4 waves x 1 beats 2 waves x 2 by 8%);
-// - gate_up with two token tiles runs 27% faster on single-block chunks, its operands for two
-//   blocks would not fit next to each other without halving occupancy;
-// - four token tiles always take single-block chunks;
+// - gate_up with one token tile loads two k-blocks per chunk, as long as the workgroup keeps at
+//   least 3 waves; every other case loads one: gate_up with two token tiles runs 27% faster
+//   on single-block chunks (two blocks' operands would not fit next to each other without
+//   halving occupancy), and down at I=768 with 3 waves x two 1-block chunks beats 3 waves x
+//   one 2-block chunk (67.5 vs 70 us at 128 tokens, 78.5 vs 85.6 at 256);
 // - 4 waves per workgroup beat 8 (gate_up at 128 tokens 135.8 -> 127.5 us, E=512 494 -> 476 us
 //   for the layer): each wave then walks two chunks, and four workgroups share a CU.
 // W = the largest divisor of the chunk count up to 4, so every wave gets the same k-blocks.
@@ -62,16 +62,16 @@ inline SplitPlan split_plan(int nkb, int TT, bool down) {
     while (chunks % w != 0) --w;
     return w;
   };
-  const bool pairs = nkb % 2 == 0 && (TT == 1 || (TT == 2 && down));
+  const bool pairs = !down && TT == 1 && nkb % 2 == 0;
   if (pairs && waves_for(nkb / 2) >= 3) return {waves_for(nkb / 2), 2};
   return {waves_for(nkb), 1};
 }
 
 // Calls f.template operator()<TT, MAXB>() for the plan's MAXB (split_plan gives MAXB = 2 only
-// for one or two token tiles).
+// for one token tile).
 template <int TT, typename F>
 inline hipError_t with_maxb(const SplitPlan& plan, F&& f) {
-  if constexpr (TT <= 2) {
+  if constexpr (TT == 1) {
     if (plan.maxb == 2) return f.template operator()<TT, 2>();
   }
   return f.template operator()<TT, 1>();

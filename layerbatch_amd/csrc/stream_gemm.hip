@@ -81,10 +81,7 @@ __device__ __forceinline__ void split_mma(u32x4* __restrict__ slot, const u32x4 
 }
 
 // This wave's share of the item: acc = sum over k-blocks [kb0, kb0 + per) in chunks of MAXB.
-// ALL_FIRST issues every load of a chunk before its first MFMA at the cost of occupancy,
-// which pays off for down with two token tiles (80 instead of 111 us at 256 tokens); elsewhere
-// the compiler's interleaving at higher occupancy is faster.
-template <int TT, int MAXB, bool ALL_FIRST>
+template <int TT, int MAXB>
 __device__ __forceinline__ void split_dot(u32x4* __restrict__ slot, const char* const (&abase)[2],
                                           int astep, uint32_t aoff,
                                           const uint16_t* const (&bp)[TT][4], int kb0, int per,
@@ -97,9 +94,6 @@ __device__ __forceinline__ void split_dot(u32x4* __restrict__ slot, const char* 
     u32x4 a[MAXB][2][4], b[MAXB][TT][4];
 #pragma unroll
     for (int m = 0; m < MAXB; ++m) split_load<TT>(abase, astep, aoff, bp, kb + m, a[m], b[m]);
-    // keep every load of the chunk ahead of its first MFMA (the scheduler would otherwise
-    // defer some to save registers)
-    if constexpr (ALL_FIRST) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < MAXB; ++m) split_mma<TT>(slot, a[m], b[m], acc);
   }
@@ -335,7 +329,7 @@ hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, c
 // that a typical expert's weights stream once, few enough to keep occupancy.
 static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
   const double avg = gw.g0 < gw.E ? static_cast<double>(T) * k / gw.E : static_cast<double>(T);
-  if (avg <= 12.0) return 1;
+  if (avg <= 8.0) return 1;   // above, many groups would need two passes of 16 tokens
   if (avg <= 28.0) return 2;
   return 4;
 }
@@ -387,7 +381,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
         bp[j][u] = x + static_cast<int64_t>(tok) * H + 8 * r;
       }
     f32x4 acc[2][TT];
-    split_dot<TT, MAXB, false>(lds + wv * 256, abase, 4 * H * 2, aoff, bp, wv * per, per, acc);
+    split_dot<TT, MAXB>(lds + wv * 256, abase, 4 * H * 2, aoff, bp, wv * per, per, acc);
     split_publish<TT>(lds, wv, acc);
     for (int t = threadIdx.x; t < 64 * TT; t += blockDim.x) {   // (token tile j, lane)
       const int j = t >> 6;
@@ -466,7 +460,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
         bp[j][u] = act + static_cast<int64_t>(row0 + p) * act_ld + 8 * r;
       }
     f32x4 acc[2][TT];
-    split_dot<TT, MAXB, TT == 2>(lds + wv * 256, abase, 4 * Ig * 2, aoff, bp, wv * per, per, acc);
+    split_dot<TT, MAXB>(lds + wv * 256, abase, 4 * Ig * 2, aoff, bp, wv * per, per, acc);
     split_publish<TT>(lds, wv, acc);
     for (int t = threadIdx.x; t < 2 * 64 * TT; t += blockDim.x) {   // (tile i, token tile j, lane)
       const int i = t >> 6 & 1, j = t >> 7;
