@@ -94,6 +94,20 @@ def test_fullsize_decode_qwen3_30b(gpu, T):
     _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=1, zipf=False, sample=24)
 
 
+# either side of the kernel switches: one token tile (up to 8 tokens per expert) / two / the
+# LDS-tiled GEMMs (from 28), and the single-workgroup permutation (up to 4096 entries)
+@pytest.mark.parametrize("T", [1, 136, 448, 449, 513])
+def test_fullsize_qwen3_30b_path_boundaries(gpu, T):
+    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=T, zipf=False, sample=12)
+
+
+@pytest.mark.parametrize("T", [16, 1100])
+def test_fullsize_e512_streaming_shared_slices(gpu, T):
+    """E=512 with the shared expert's token passes spread over extra workgroup rows (T=1100:
+    streaming with two token tiles, 35 passes on 16 slices)."""
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=T, zipf=False, sample=12)
+
+
 def test_fullsize_prefill_qwen3_30b_zipf(gpu):
     """The same layer at T=8192 with the Zipf(1.2) router bias: empty experts, a hot expert
     with thousands of tokens, wide and narrow tiles."""
