@@ -21,7 +21,11 @@ and decoder layer (qwen3_5.py:956-962, :1004) use them unchanged. Differences, a
 * ``Qwen3_5TopKRouter.logit_bias`` (default None) is an optional fp32 [E] tensor added to
   the upcast logits before the softmax; it is not a checkpoint parameter.
 * ``Qwen3_5SparseMoeBlock.quantize_fp8_()`` converts the expert and shared-expert weights to
-  OCP e4m3fn with per-128x128-block fp32 scales (no counterpart in the reference).
+  OCP e4m3fn with per-128x128-block fp32 scales (no counterpart in the reference);
+  ``load_fp8_`` installs codes and scales computed elsewhere (layerbatch_amd/checkpoint.py).
+* ``Qwen3_5SparseMoeBlock.forward_norm(hidden, residual, norm)`` runs the decoder layer's
+  residual add, post_attention_layernorm and the block in one call (qwen3_5.py:998-1004),
+  returning (block output, new residual).
 
 Every forward runs on the tensor's CUDA (HIP) device on the current stream, enqueues HIP
 kernels only (no host synchronisation), and raises RuntimeError for CPU tensors, wrong dtypes
@@ -52,8 +56,39 @@ def _require(t, name, dtype=torch.bfloat16, ndim=None):
         raise RuntimeError(f"{name} must be contiguous")
 
 
-def _workspace(layer, T, device):
-    return torch.empty(_lib.workspace_size(layer, T), dtype=torch.uint8, device=device)
+def _device_tensors(module):
+    """Every tensor a module's kernels read: parameters and installed fp8 codes and scales."""
+    for p in module.parameters():
+        yield p
+    for m in module.modules():
+        for name in ("gate_up_q", "gate_up_scale", "down_q", "down_scale", "logit_bias"):
+            t = getattr(m, name, None)
+            if isinstance(t, torch.Tensor):
+                yield t
+        q = getattr(m, "q", None)
+        if isinstance(q, dict):
+            for codes, scales in q.values():
+                yield codes
+                yield scales
+
+
+def _same_device(module, device):
+    """The kernels dereference the module's tensors on the input's device: refuse a mix."""
+    for t in _device_tensors(module):
+        if t.device != device:
+            raise RuntimeError(f"a {type(module).__name__} tensor is on {t.device}, the input on "
+                               f"{device}: move the module to the input's device")
+
+
+def _workspace(layer, T, device, workspace=None):
+    """The caller's workspace (checked: uint8, contiguous, on the input's device; the library
+    checks its size), or a new one from torch's caching allocator."""
+    if workspace is None:
+        return torch.empty(_lib.workspace_size(layer, T), dtype=torch.uint8, device=device)
+    _require(workspace, "workspace", torch.uint8)
+    if workspace.device != device:
+        raise RuntimeError(f"workspace is on {workspace.device}, the input on {device}")
+    return workspace
 
 
 class Qwen3_5TopKRouter(nn.Module):
@@ -84,6 +119,7 @@ class Qwen3_5TopKRouter(nn.Module):
         """bf16 router logits [T, E] (the F.linear of qwen3_5.py:769)."""
         _require(hidden_states, "hidden_states", ndim=2)
         _require(self.weight, "gate.weight", ndim=2)
+        _same_device(self, hidden_states.device)
         T = hidden_states.shape[0]
         out = torch.empty((T, self.num_experts), dtype=torch.bfloat16, device=hidden_states.device)
         L = self._layer()
@@ -150,6 +186,10 @@ class Qwen3_5Experts(nn.Module):
         T, k = top_k_indices.shape
         if hidden_states.shape[0] != T or tuple(top_k_weights.shape) != (T, k):
             raise RuntimeError("hidden_states / top_k_indices / top_k_weights disagree on [T, k]")
+        dev = hidden_states.device
+        if top_k_indices.device != dev or top_k_weights.device != dev:
+            raise RuntimeError("hidden_states, top_k_indices and top_k_weights must share a device")
+        _same_device(self, dev)
         L = LbmoeLayer()
         self.fill_layer(L)
         L.top_k = k
@@ -193,6 +233,7 @@ class Qwen3_5SharedExpertMLP(nn.Module):
 
     def forward(self, x):
         _require(x, "x", ndim=2)
+        _same_device(self, x.device)
         T, H = x.shape
         Is = self.gate_proj.weight.shape[0]
         (g, u, d), (gs, us, ds) = self._ptrs()
@@ -259,11 +300,11 @@ class Qwen3_5SparseMoeBlock(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, workspace: torch.Tensor = None):
         _require(hidden_states, "hidden_states", ndim=2)
+        _same_device(self, hidden_states.device)
         T = hidden_states.shape[0]
         L = self.layer()
         dev = hidden_states.device
-        if workspace is None:
-            workspace = _workspace(L, T, dev)
+        workspace = _workspace(L, T, dev, workspace)
         y = torch.empty_like(hidden_states)
         with torch.cuda.device(dev):
             check(lib().lbmoe_forward(ctypes.byref(L), ptr(hidden_states), T, ptr(y),
@@ -286,11 +327,13 @@ class Qwen3_5SparseMoeBlock(nn.Module):
         _require(norm.weight, "norm.weight", ndim=1)
         if residual.shape != hidden_states.shape:
             raise RuntimeError("hidden_states and residual must have the same shape")
+        if residual.device != hidden_states.device or norm.weight.device != hidden_states.device:
+            raise RuntimeError("hidden_states, residual and norm.weight must share a device")
+        _same_device(self, hidden_states.device)
         T = hidden_states.shape[0]
         L = self.layer()
         dev = hidden_states.device
-        if workspace is None:
-            workspace = _workspace(L, T, dev)
+        workspace = _workspace(L, T, dev, workspace)
         y = torch.empty_like(hidden_states)
         new_residual = torch.empty_like(residual)
         with torch.cuda.device(dev):

@@ -228,6 +228,28 @@ def test_cpu_tensor_raises(gpu):
         blk(torch.zeros((4, 1024), dtype=torch.bfloat16))
 
 
+def test_host_checks_before_any_launch(gpu):
+    """Weights left on the CPU, a workspace of the wrong dtype or size: refused on the host."""
+    shape = SHAPES["small-h1024-e16"]
+    w, g = make_layer(shape)
+    x = make_x(g, 8, shape.hidden_size).to(gpu)
+    cpu_blk = _block(shape, w, "cpu")
+    with pytest.raises(RuntimeError, match="device"):
+        cpu_blk(x)
+    with pytest.raises(RuntimeError, match="device"):
+        cpu_blk.experts(x, torch.zeros((8, 2), dtype=torch.int64, device=gpu),
+                        torch.zeros((8, 2), dtype=torch.bfloat16, device=gpu))
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    n = blk.workspace_size(8)
+    with pytest.raises(RuntimeError, match="uint8"):
+        blk(x, workspace=torch.empty(n, dtype=torch.float32, device=gpu))
+    with pytest.raises(RuntimeError):
+        blk(x, workspace=torch.empty(n - 1, dtype=torch.uint8, device=gpu))
+    y = blk(x, workspace=torch.empty(n, dtype=torch.uint8, device=gpu))   # the exact size works
+    torch.cuda.synchronize()
+    assert y.shape == x.shape
+
+
 @pytest.mark.parametrize("T,E,k,levels,bias", [(300, 128, 8, 3, False), (257, 512, 10, 4, False),
                                                (64, 1000, 32, 2, True), (100, 64, 32, 5, False),
                                                (77, 200, 7, 1, True), (129, 16, 2, 2, False)])
