@@ -12,19 +12,25 @@ pytestmark = pytest.mark.gpu
 SHAPE = MoEShape(1024, 16, 2, 512, 256)
 
 
-def _setup(gpu, T, seed=3, fp8=False):
-    w, g = make_layer(SHAPE, seed=seed)
-    blk = _block(SHAPE, {k: v.to(gpu) for k, v in w.items()}, gpu)
+# a layer with 64 experts, top-8 and a shared expert: 1600 (token, slot) pairs at T=200 take the
+# single-workgroup permutation with two entries per thread, the shared expert 7 slices
+WIDE = MoEShape(1024, 64, 8, 256, 256)
+
+
+def _setup(gpu, T, seed=3, fp8=False, shape=SHAPE):
+    w, g = make_layer(shape, seed=seed)
+    blk = _block(shape, {k: v.to(gpu) for k, v in w.items()}, gpu)
     if fp8:
         blk.quantize_fp8_()
-    xs = [make_x(g, T, SHAPE.hidden_size).to(gpu) for _ in range(3)]
+    xs = [make_x(g, T, shape.hidden_size).to(gpu) for _ in range(3)]
     return blk, xs
 
 
 # streaming GEMMs, LDS-tiled GEMMs; bf16 and fp8 weights
-@pytest.mark.parametrize("T,fp8", [(40, False), (512, False), (40, True), (512, True)])
-def test_graph_replay_matches_eager(gpu, T, fp8):
-    blk, xs = _setup(gpu, T, fp8=fp8)
+@pytest.mark.parametrize("T,fp8,shape", [(40, False, SHAPE), (512, False, SHAPE), (40, True, SHAPE),
+                                         (512, True, SHAPE), (200, False, WIDE)])
+def test_graph_replay_matches_eager(gpu, T, fp8, shape):
+    blk, xs = _setup(gpu, T, fp8=fp8, shape=shape)
     ws_e = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device=gpu)
     ws_g = torch.empty_like(ws_e)
     static_x = xs[0].clone()
