@@ -6,7 +6,9 @@
 // weight rows by a tile of tokens of one expert, staging both operands
 // through LDS in k-tiles, so each operand byte fetched from L2 feeds many MFMA columns. The
 // k-tiles move global -> LDS directly (global_load_lds_dwordx4, no register staging) through
-// a ring of LDS buffers that is filled kStages k-tiles ahead of the MFMAs.
+// a ring of LDS buffers that is filled kStages k-tiles ahead of the MFMAs. The wide tiles'
+// weight operand has one stage more than its token operand (3 + 2 stages of 32 KB, the CU's
+// whole 160 KB): the weight copies, which may stream from HBM, get a k-tile longer to land.
 //
 // Two token-tile widths share one launch. A wide tile (256 tokens, each wave 128 x 64) moves
 // the fewest operand bytes per flop, which matters here: with the whole chip busy the shader
@@ -39,7 +41,10 @@ namespace lbmoe {
 #define LBMOE_TILE_BK 64
 #endif
 #ifndef LBMOE_TILE_STAGES
-#define LBMOE_TILE_STAGES 2
+#define LBMOE_TILE_STAGES 3
+#endif
+#ifndef LBMOE_TILE_BSTAGES
+#define LBMOE_TILE_BSTAGES 2
 #endif
 #ifndef LBMOE_NARROW_BK
 #define LBMOE_NARROW_BK 64
@@ -48,16 +53,15 @@ namespace lbmoe {
 #define LBMOE_NARROW_STAGES 3
 #endif
 
-// wide: 2 x 4 waves of 128 x 64 (256 tokens); narrow: 2 x 4 waves of 128 x 32 (128 tokens)
-using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES>;
+// wide: 2 x 4 waves of 128 x 64 (256 tokens), 3 weight + 2 token stages; narrow: 2 x 4 waves
+// of 128 x 32 (128 tokens), 3 stages of both
+using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES, LBMOE_TILE_BSTAGES>;
 using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
 // router logits: 4 x 2 waves of 64 x 32 (256 experts x 64 tokens); for at most 128 experts
 // 4 x 2 waves of 32 x 32 (128 x 64) with a ring small enough for two workgroups per CU
 using RouterShape = TileShape<4, 2, 1, 64, 3>;
 using RouterShape128 = TileShape<4, 1, 1, 64, 3>;
-constexpr int kLdsU4 = Wide::kStages * Wide::kStageU4 > Narrow::kStages * Narrow::kStageU4
-                           ? Wide::kStages * Wide::kStageU4
-                           : Narrow::kStages * Narrow::kStageU4;
+constexpr int kLdsU4 = Wide::kRingU4 > Narrow::kRingU4 ? Wide::kRingU4 : Narrow::kRingU4;
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
 
 // ---- tile list -------------------------------------------------------------------------------
@@ -306,37 +310,56 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  auto issue = [&](int stage, int k0) {
-    u32x4* buf = lds + stage * kStageU4;
+  auto issue_a = [&](int stage, int k0) {
+    u32x4* buf = lds + S::a_off(stage);
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
       __builtin_amdgcn_global_load_lds(ap[i] + k0,
                                        (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
                                        16, 0, 0);
+  };
+  auto issue_b = [&](int stage, int k0) {
+    u32x4* buf = lds + S::b_off(stage);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
       __builtin_amdgcn_global_load_lds(bp[i] + k0,
-                                       (lds_ptr)(buf + (kRows + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
+                                       (lds_ptr)(buf + ((w * kBLoads + i) * kRowsPerLoad) * kChunks),
                                        16, 0, 0);
   };
+  auto issue = [&](int stage, int k0) {
+    issue_a(stage, k0);
+    issue_b(stage, k0);
+  };
 
-  // Ring protocol. All kStages buffers are filled up front. In k-tile kt, once this wave
+  // Ring protocol (the asymmetric ring issues A0 B0 A1 B1 A2 up front, then refills B kt+2
+  // and A kt+3 after k-tile kt, so at the end of k-tile kt only A kt+2 is younger than the
+  // copies of k-tile kt+1). Otherwise all kStages buffers are filled up front. In k-tile kt, once this wave
   // has read the last k-step's fragments of stage kt, it waits for its copies of stage kt+1,
   // meets the other waves at the barrier (after which nobody reads stage kt any more), reads
   // stage kt+1's first fragments and refills stage kt's buffer with k-tile kt+kStages, all
   // interleaved with the last k-step's MFMAs, so neither the copy issue nor the LDS read
   // latency of the next k-tile stands between two MFMAs.
   const int nk = K / kBK;
+  if constexpr (S::kAsym) {
 #pragma unroll
-  for (int st = 0; st < kStages; ++st)
-    if (st < nk) issue(st, st * kBK);
+    for (int st = 0; st < kStages; ++st) {
+      if (st < nk) issue_a(st, st * kBK);
+      if (st < S::kBStages && st < nk) issue_b(st, st * kBK);
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < kStages; ++st)
+      if (st < nk) issue(st, st * kBK);
+  }
   const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
-  auto read_frags = [&](const u32x4* cur, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
+  auto read_frags = [&](int kt, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
     const int j = 2 * ks + mk;
+    const u32x4* ca = lds + S::a_off(kt % kStages);
+    const u32x4* cb = lds + S::b_off(kt % S::kBStages);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) fa[i] = cur[S::swz(wm * kRW + 32 * i + mr, j)];
+    for (int i = 0; i < kMT; ++i) fa[i] = ca[S::swz(wm * kRW + 32 * i + mr, j)];
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) fb[t] = cur[S::swz(kRows + wn * (kNT * 32) + 32 * t + mr, j)];
+    for (int t = 0; t < kNT; ++t) fb[t] = cb[S::swz(wn * (kNT * 32) + 32 * t + mr, j)];
   };
   auto mfma_all = [&](const u32x4 (&fa)[kMT], const u32x4 (&fb)[kNT]) {
 #pragma unroll
@@ -359,13 +382,13 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   };
   u32x4 fa[2][kMT], fb[2][kNT];
   // One k-tile. NEXT: a k-tile follows (wait, barrier, read its first fragments); REFILL: the
-  // freed buffer takes k-tile kt + kStages. Specialised at compile time so that the loop body
+  // freed buffers take k-tile kt + kStages (2: both operands; 1: the asymmetric ring's token
+  // operand only, whose ring runs one k-tile shorter). Specialised at compile time so that the loop body
   // has no branches around the MFMAs.
-  auto ktile = [&]<bool NEXT, bool REFILL>(int kt) {
-    const u32x4* cur = lds + (kt % kStages) * kStageU4;
+  auto ktile = [&]<bool NEXT, int REFILL>(int kt) {
 #pragma unroll
     for (int ks = 0; ks + 1 < kKSteps; ++ks) {
-      read_frags(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      read_frags(kt, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       mfma_all(fa[ks & 1], fb[ks & 1]);
       sched_reads();
       if constexpr (kMfmas > kPaired) __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPaired, 0);
@@ -374,17 +397,28 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     if constexpr (NEXT) {
       // all earlier MFMAs stay above the barrier: they cover the last fragment reads' latency
       __builtin_amdgcn_sched_barrier(0);
-      wait_ring<kStages - 2, kLoads>(nk - 2 - kt);
+      if constexpr (S::kAsym) {
+        // k-tile kt+1 must have landed; only the weight copies of k-tile kt+2 may be younger
+        if (kt + 2 < nk) wait_vmcnt<kALoads>();
+        else wait_vmcnt<0>();
+      } else {
+        wait_ring<kStages - 2, kLoads>(nk - 2 - kt);
+      }
       ring_barrier();
-      read_frags(lds + ((kt + 1) % kStages) * kStageU4, 0, fa[0], fb[0]);
-      if constexpr (REFILL) issue(kt % kStages, (kt + kStages) * kBK);
+      read_frags(kt + 1, 0, fa[0], fb[0]);
+      if constexpr (S::kAsym) {
+        if constexpr (REFILL >= 1) issue_b(kt % S::kBStages, (kt + S::kBStages) * kBK);
+        if constexpr (REFILL >= 2) issue_a(kt % kStages, (kt + kStages) * kBK);
+      } else {
+        if constexpr (REFILL >= 2) issue(kt % kStages, (kt + kStages) * kBK);
+      }
     }
     mfma_all(fa[kl], fb[kl]);
     if constexpr (NEXT) {
       // next k-tile's first reads with the first MFMAs, then the copies spread over the rest
       sched_reads();
       constexpr int kRest = kMfmas - kPaired;
-      if constexpr (REFILL && kRest > 0) {
+      if constexpr (REFILL > 0 && kRest > 0) {
         constexpr int kPer = (kLoads + kRest - 1) / (kRest > 0 ? kRest : 1);
 #pragma unroll
         for (int r = 0; r < kRest; ++r) {
@@ -394,13 +428,22 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       }
     }
   };
-  wait_ring<kStages - 1, kLoads>(nk - 1);
+  if constexpr (S::kAsym) {
+    // k-tile 0 must have landed; younger: k-tile 1 (both operands) and k-tile 2's weights
+    if (nk > 2) wait_vmcnt<kLoads + kALoads>();
+    else if (nk > 1) wait_vmcnt<kLoads>();
+    else wait_vmcnt<0>();
+  } else {
+    wait_ring<kStages - 1, kLoads>(nk - 1);
+  }
   ring_barrier();
-  read_frags(lds, 0, fa[0], fb[0]);
+  read_frags(0, 0, fa[0], fb[0]);
   int kt = 0;
-  for (; kt + kStages < nk; ++kt) ktile.template operator()<true, true>(kt);
-  for (; kt + 1 < nk; ++kt) ktile.template operator()<true, false>(kt);
-  ktile.template operator()<false, false>(kt);
+  for (; kt + kStages < nk; ++kt) ktile.template operator()<true, 2>(kt);
+  if constexpr (S::kAsym)
+    for (; kt + S::kBStages < nk; ++kt) ktile.template operator()<true, 1>(kt);
+  for (; kt + 1 < nk; ++kt) ktile.template operator()<true, 0>(kt);
+  ktile.template operator()<false, 0>(kt);
 
   // Epilogue.
   const int col = lane & 31, rq = 4 * (lane >> 5);
@@ -464,11 +507,11 @@ template <class S>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
 void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T, int n_wtiles,
                          uint16_t* __restrict__ logits) {
-  __shared__ u32x4 lds[S::kStages * S::kStageU4];
+  __shared__ u32x4 lds[S::kRingU4];
   const int logical = xcd_item(blockIdx.x, (T + S::kWT - 1) / S::kWT * n_wtiles);
   if (logical < 0) return;
   const int ti = logical / n_wtiles, wt = logical - ti * n_wtiles;
-  tile_product<kRouter, S, S::kStages * S::kStageU4>(gw, x, gw.H, nullptr, 0, ti * S::kWT, T, 0,
+  tile_product<kRouter, S, S::kRingU4>(gw, x, gw.H, nullptr, 0, ti * S::kWT, T, 0,
                                                      wt, logits, gw.E, lds);
 }
 

@@ -18,9 +18,11 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kWM = 256;                            // weight rows per workgroup
 
 // One token-tile shape: WAVES_M x (kWaves / WAVES_M) waves, each owning MT x NT units of 32
-// weight rows x 32 tokens, k-tiles of BK bf16 (2 * BK bytes per row), STAGES LDS buffers. The
+// weight rows x 32 tokens, k-tiles of BK bf16 (2 * BK bytes per row), STAGES LDS buffers of
+// the weight operand and BSTAGES (STAGES or STAGES - 1) of the token operand. A symmetric ring
+// interleaves the operands per stage; an asymmetric one keeps all weight stages first. The
 // expert GEMMs use kRows = kWM weight rows; the router may use fewer.
-template <int WAVES_M, int MT, int NT, int BK, int STAGES>
+template <int WAVES_M, int MT, int NT, int BK, int STAGES, int BSTAGES = STAGES>
 struct TileShape {
   static constexpr int kRows = WAVES_M * MT * 32;             // weight rows per workgroup
   static constexpr int kWavesM = WAVES_M;
@@ -31,12 +33,19 @@ struct TileShape {
   static constexpr int kWT = kWavesN * NT * 32;               // tokens per workgroup
   static constexpr int kBK = BK;
   static constexpr int kStages = STAGES;
+  static constexpr int kBStages = BSTAGES;
   static constexpr int kChunks = BK / 8;                      // 16-byte chunks per LDS row
   static constexpr int kRowsPerLoad = 64 / kChunks;           // rows one wave copy covers
   static constexpr int kALoads = kRows / kRowsPerLoad / kWaves;  // wave copies per stage (weights)
   static constexpr int kBLoads = kWT / kRowsPerLoad / kWaves;  // wave copies per stage (tokens)
   static constexpr int kLoads = kALoads + kBLoads;
   static constexpr int kStageU4 = (kRows + kWT) * kChunks;    // 16-byte slots per stage
+  static constexpr int kAU4 = kRows * kChunks, kBU4 = kWT * kChunks;
+  static constexpr bool kAsym = BSTAGES != STAGES;
+  static constexpr int kRingU4 = kAsym ? STAGES * kAU4 + BSTAGES * kBU4 : STAGES * kStageU4;
+  static_assert(!kAsym || BSTAGES + 1 == STAGES, "asymmetric ring: one more weight stage");
+  static constexpr int a_off(int s) { return kAsym ? s * kAU4 : s * kStageU4; }
+  static constexpr int b_off(int s) { return kAsym ? STAGES * kAU4 + s * kBU4 : s * kStageU4 + kAU4; }
   static constexpr int kKSteps = BK / 16;                     // bf16 MFMA k-steps per k-tile
   // Chunk j of row r lives at slot r*kChunks + (j ^ f(r)), f(r) = (r / (16/kChunks)) mod
   // kChunks: 16 consecutive rows then hit 16 distinct 16-byte bank groups for any fixed j.
