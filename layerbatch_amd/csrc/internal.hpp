@@ -104,8 +104,8 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,
                           void* y, hipStream_t s);
-// LDS-tiled grouped GEMMs (prefill-sized batches) over a tile list of wide and narrow token
-// tiles, with one dispatch table per GEMM launch (bf16 and fp8 kernels share both).
+// LDS-tiled grouped GEMMs (prefill-sized batches) over a tile list of wide, narrow and tiny
+// token tiles, with one dispatch table per GEMM launch (bf16 and fp8 kernels share both).
 // Words behind a tile list's entries: count, wide count.
 constexpr int kTileListTail = 2;
 int tiled_max_tiles(int64_t rows, int groups);  // rows = routed + shared

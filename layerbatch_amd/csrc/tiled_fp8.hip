@@ -338,7 +338,7 @@ void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
   __shared__ float scl[kActScales + kWScales];
   const TileItem it = decode_item(table[blockIdx.x]);
   if (it.g < 0) return;
-  if (it.narrow)
+  if (it.narrow || it.tiny)        // a tiny tile's rows are a narrow tile's first rows
     tile_product_fp8<GATEUP, Narrow>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
                                      it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
   else

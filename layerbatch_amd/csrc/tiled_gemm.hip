@@ -15,11 +15,13 @@
 // clock settles near 1.5 GHz and every byte moved between L2 and LDS costs cycles and power.
 // A narrow tile (128 tokens, each wave 128 x 32) serves the few tokens that small experts get
 // under a skewed router: such a tile is bound by streaming the expert's weights from HBM, and
-// a wide tile would spend twice the MFMA work on padding. Because the tile list follows expert
-// order, narrow (HBM-bound) and wide (MFMA-bound) tiles run side by side.
+// a wide tile would spend twice the MFMA work on padding. A tiny tile (64 tokens, each wave
+// 64 x 32) takes a group's last rows when there are at most 64 of them, which under a skewed
+// router is most experts. Because the tile list follows expert order, narrow and tiny
+// (HBM-bound) and wide (MFMA-bound) tiles run side by side.
 //
 // Work list. build_tiles turns the per-expert token counts into a list of (group, first row |
-// narrow flag) token tiles, wide ones first; a launch has one workgroup per possible
+// narrow or tiny flag) token tiles, wide ones first; a launch has one workgroup per possible
 // (token tile, weight tile) item (a function of T only), and dispatch_item maps workgroups to
 // items so that each XCD works on its own share, with small-expert tiles spread over the
 // launch and its last round.
@@ -57,28 +59,34 @@ namespace lbmoe {
 // of 128 x 32 (128 tokens), 3 stages of both
 using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES, LBMOE_TILE_BSTAGES>;
 using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
+// tiny: 4 x 2 waves of 64 x 32 (64 tokens), for a group's last few rows
+using Tiny = TileShape<4, 2, 1, 64, 3>;
 // router logits: 4 x 2 waves of 64 x 32 (256 experts x 64 tokens); for at most 128 experts
 // 4 x 2 waves of 32 x 32 (128 x 64) with a ring small enough for two workgroups per CU
 using RouterShape = TileShape<4, 2, 1, 64, 3>;
 using RouterShape128 = TileShape<4, 1, 1, 64, 3>;
 constexpr int kLdsU4 = Wide::kRingU4 > Narrow::kRingU4 ? Wide::kRingU4 : Narrow::kRingU4;
+static_assert(Tiny::kRingU4 <= kLdsU4, "tiny ring exceeds the others");
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
 
 // ---- tile list -------------------------------------------------------------------------------
 // tiles[2i] = group, tiles[2i+1] = first row within the group (| kNarrowFlag for a narrow
-// tile). All wide tiles come first, in group order, then all narrow tiles, in group order.
+// tile, | kTinyFlag for a tiny one). All wide tiles come first, in group order, then all
+// narrow and tiny tiles, in group order.
 // Behind the max_tiles entries: tiles[2*max_tiles] = number of valid entries,
 // tiles[2*max_tiles+1] = number of wide entries. Groups: routed experts 0..E-1 with counts[g]
 // rows, then the shared expert (T rows) when present. A group of n rows gets n / wide wide
 // tiles; the remainder r is one more wide tile when r > wide - narrow (or when narrow == 0),
-// else ceil(r / narrow) narrow tiles.
-__device__ __forceinline__ void group_tiles(int n, int wide, int narrow, int& n_wide,
-                                            int& n_narrow) {
+// else one tiny tile when r <= tiny, else ceil(r / narrow) narrow tiles.
+__device__ __forceinline__ void group_tiles(int n, int wide, int narrow, int tiny, int& n_wide,
+                                            int& n_narrow, int& n_tiny) {
   n_wide = n / wide;
   n_narrow = 0;
+  n_tiny = 0;
   const int r = n - n_wide * wide;
   if (r == 0) return;
   if (narrow == 0 || r > wide - narrow) ++n_wide;
+  else if (r <= tiny) n_tiny = 1;
   else n_narrow = (r + narrow - 1) / narrow;
 }
 
@@ -106,7 +114,7 @@ __device__ __forceinline__ int block_scan_1024(int v, int& excl, int* wsum) {
 }
 
 // Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
-// fastest; the W wide items come first, then the N narrow ones. XCD x owns the x-th contiguous
+// fastest; the W wide items come first, then the N narrow and tiny ones (both "narrow" below). XCD x owns the x-th contiguous
 // eighth of the wide items and of the narrow items, so items that share a token tile run on
 // one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
 // (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
@@ -167,7 +175,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
                                                            const int32_t* __restrict__ offsets,
                                                            int E, int shared, int T, int sh_row0,
                                                            int max_tiles, int wide, int narrow,
-                                                           int I, int Is, int H, int grid_gu,
+                                                           int tiny, int I, int Is, int H, int grid_gu,
                                                            int grid_dn, int32_t* __restrict__ tiles) {
   __shared__ int wsum[16];
   __shared__ int s_list[2 * kLdsListEntries];
@@ -177,13 +185,13 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   const bool in_lds = max_tiles <= kLdsListEntries;
   const int per = (G + 1023) / 1024;
   const int lo = min(G, tid * per), hi = min(G, lo + per);
-  int lw = 0, ln = 0, nw, nn;
+  int lw = 0, ln = 0, nw, nn, nt;
   for (int g = lo; g < hi; ++g) {
     const int n = g < E ? counts[g] : T;
     s_grp[g] = int2{g < E ? offsets[g] : sh_row0, n};
-    group_tiles(n, wide, narrow, nw, nn);
+    group_tiles(n, wide, narrow, tiny, nw, nn, nt);
     lw += nw;
-    ln += nn;
+    ln += nn + nt;
   }
   int pw, pn;
   const int tw = block_scan_1024(lw, pw, wsum);
@@ -199,9 +207,10 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     }
   };
   for (int g = lo; g < hi; ++g) {
-    group_tiles(s_grp[g].y, wide, narrow, nw, nn);
+    group_tiles(s_grp[g].y, wide, narrow, tiny, nw, nn, nt);
     for (int i = 0; i < nw; ++i) put(pw++, g, i * wide);
     for (int i = 0; i < nn; ++i) put(pn++, g, (nw * wide + i * narrow) | kNarrowFlag);
+    if (nt) put(pn++, g, (nw * wide) | kTinyFlag);
   }
   const int n_all = min(tw + tn, max_tiles), n_wide = min(tw, max_tiles);
   if (tid == 0) {
@@ -523,7 +532,10 @@ void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
   __shared__ u32x4 lds[kLdsU4];
   const TileItem it = decode_item(table[blockIdx.x]);
   if (it.g < 0) return;
-  if (it.narrow)
+  if (it.tiny)
+    tile_product<MODE, Tiny>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n, it.row0, it.wt, dst,
+                             dst_ld, lds);
+  else if (it.narrow)
     tile_product<MODE, Narrow>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n, it.row0, it.wt,
                                dst, dst_ld, lds);
   else
@@ -575,7 +587,7 @@ hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, con
                               hipStream_t s) {
   build_tiles_kernel<<<1, 1024, 0, s>>>(counts, offsets, gw.E, shared ? 1 : 0,
                                         static_cast<int>(T), gw.sh_row0, max_tiles, Wide::kWT,
-                                        Narrow::kWT, gw.I, gw.Is, gw.H,
+                                        Narrow::kWT, Tiny::kWT, gw.I, gw.Is, gw.H,
                                         tiled_grid(gw, max_tiles, true),
                                         tiled_grid(gw, max_tiles, false), tiles);
   return hipGetLastError();

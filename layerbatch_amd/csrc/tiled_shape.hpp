@@ -59,8 +59,9 @@ struct TileShape {
   }
 };
 
-// Narrow token tiles carry this flag on their first row.
+// Narrow and tiny token tiles carry these flags on their first row.
 constexpr int32_t kNarrowFlag = 1 << 30;
+constexpr int32_t kTinyFlag = 1 << 29;
 
 // One dispatch-table entry (16 bytes, written by build_tiles_kernel): the work of one
 // workgroup of a GEMM launch.
@@ -69,6 +70,7 @@ struct TileItem {
   int wt;       // weight tile
   int r0;       // first row of the token tile within the group
   bool narrow;  // narrow token tile
+  bool tiny;    // tiny token tile (a group's last rows, at most a tiny tile's width)
   int row0;     // the group's first row in the expert-sorted rows
   int n;        // the group's row count
 };
@@ -79,7 +81,8 @@ __device__ __forceinline__ TileItem decode_item(u32x4 ent) {
   it.wt = gx >> 16;
   const int e = static_cast<int>(ent[1]);
   it.narrow = (e & kNarrowFlag) != 0;
-  it.r0 = e & (kNarrowFlag - 1);
+  it.tiny = (e & kTinyFlag) != 0;
+  it.r0 = e & (kTinyFlag - 1);
   it.row0 = static_cast<int>(ent[2]);
   it.n = static_cast<int>(ent[3]);
   return it;

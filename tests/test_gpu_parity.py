@@ -332,3 +332,44 @@ def test_forward_norm_rejects_in_place_residual(gpu, lbmoe):
     st = lbmoe.lbmoe_forward_norm(ctypes.byref(L), _lib.ptr(hid), _lib.ptr(res), _lib.ptr(nw), 1e-6, 8,
                                   _lib.ptr(y), _lib.ptr(res), _lib.ptr(ws), ws.numel(), _lib.stream_of(gpu))
     assert st == -2
+
+
+# rows per expert chosen so that the tiled GEMMs see every token-tile class boundary: a group's
+# last rows r after its full 256-row tiles are r <= 64 (one 64-row tile), 64 < r <= 128 (one
+# 128-row tile) or r > 128 (one more 256-row tile)
+TILE_BOUNDARY_COUNTS = [0, 1, 63, 64, 65, 127, 128, 129, 130, 255, 256, 257, 320, 384, 385, 512]
+
+
+def _boundary_routing(seed):
+    """k = 1 routing with exactly TILE_BOUNDARY_COUNTS[e] tokens on expert e, tokens shuffled,
+    and random bf16 weights."""
+    counts = np.array(TILE_BOUNDARY_COUNTS)
+    T = int(counts.sum())
+    rng = np.random.default_rng(seed)
+    idx = rng.permutation(np.repeat(np.arange(len(counts)), counts)).reshape(T, 1)
+    tw = torch.from_numpy(rng.uniform(0.05, 1.0, size=(T, 1))).to(torch.bfloat16)
+    return T, idx.astype(np.int64), tw
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_experts_tile_class_boundaries(gpu, fp8):
+    shape = MoEShape(512, len(TILE_BOUNDARY_COUNTS), 1, 256, 0)
+    T, idx, tw = _boundary_routing(31)
+    w, g = make_layer(shape, seed=12)
+    x = make_x(g, T, shape.hidden_size)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    if fp8:
+        blk.quantize_fp8_()
+    y = blk.experts(x.to(gpu), torch.from_numpy(idx).to(gpu), tw.to(gpu))
+    torch.cuda.synchronize()
+    wn = layer_np(w)
+    rows = np.arange(T)                 # every row: each tile's first and last rows matter
+    if fp8:
+        ex = blk.experts
+        y_ref = om.experts_fp8(to_np(x)[rows], idx[rows], to_np(tw)[rows], ex.gate_up_q.cpu().numpy(),
+                               ex.gate_up_scale.cpu().numpy(), ex.down_q.cpu().numpy(),
+                               ex.down_scale.cpu().numpy())
+        gc.check_output(to_np(y)[rows], y_ref, gc.TOL_FP8)
+    else:
+        y_ref = om.experts(to_np(x)[rows], idx[rows], to_np(tw)[rows], wn["gate_up"], wn["down"])
+        gc.check_output(to_np(y)[rows], y_ref, gc.TOL_BF16)
