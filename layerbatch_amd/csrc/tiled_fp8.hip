@@ -10,8 +10,9 @@
 // w_scale(row block, k-tile) * a_scale(token, k-tile) and added to the fp32 accumulator; the
 // fused multiply-adds of one MFMA step run under the next step's MFMAs.
 // Workgroup: 8 waves in 2 x 4, kWM = 256 weight rows x 256 tokens (wide: a wave owns 128 rows
-// x 64 tokens, 8 x 4 tiles of 16 x 16) or x 128 tokens (narrow: 128 x 32). Accumulator lane
-// (r, q) of a tile holds token column r and rows 4q .. 4q+3.
+// x 64 tokens, 8 x 4 tiles of 16 x 16), x 128 tokens (narrow: 128 x 32) or, on 4 x 2 waves,
+// x 64 tokens (tiny: 64 x 32). Accumulator lane (r, q) of a tile holds token column r and
+// rows 4q .. 4q+3.
 // Scales live in LDS for the whole work item: the activation scales of the tile's tokens for
 // every k-tile (one 16-byte read per lane and k-tile) and the two weight-scale rows the
 // workgroup's rows use; both are copied global -> LDS ahead of the ring's first stage.
@@ -25,8 +26,10 @@ namespace f8t {
 // The LDS ring of 128-byte k-tiles (TileShape counts k-tiles in bf16 units: BK = 64).
 using Wide = TileShape<2, 4, 2, 64, 2>;
 using Narrow = TileShape<2, 4, 1, 64, 2>;
+using Tiny = TileShape<4, 2, 1, 64, 2>;       // 4 x 2 waves of 64 x 32: 64 tokens
 constexpr int kRingU4 = Wide::kStages * Wide::kStageU4;
 static_assert(Narrow::kStages * Narrow::kStageU4 <= kRingU4, "narrow ring exceeds the wide one");
+static_assert(Tiny::kStages * Tiny::kStageU4 <= kRingU4, "tiny ring exceeds the wide one");
 // Scale blocks per row (K / 128) the LDS scale area holds: K <= 3072.
 constexpr int kMaxKBlocks = 24;
 constexpr int kActScales = kMaxKBlocks * Wide::kWT;
@@ -74,7 +77,8 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
 
   // Weights and the two weight-scale rows (nk floats each) of the workgroup's rows. gate_up:
   // row 0 = the gate block of channels c0 .. c0+127, row 1 = their up block; down: the blocks
-  // of output columns c0 .. c0+127 and c0+128 .. c0+255 (wave row-block wm uses row wm).
+  // of output columns c0 .. c0+127 and c0+128 .. c0+255 (wave row-block wm uses row
+  // wm * kRW / 128).
   const uint8_t* wbase;
   const uint8_t* wup = nullptr;
   const float* sw0;
@@ -212,7 +216,7 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     const float* a = scl + kt * kWT + wn * (16 * kN16) + r16 * kN16;
 #pragma unroll
     for (int t = 0; t < kN16; ++t) sa[t] = a[t];
-    w0 = wsc[(GATEUP ? 0 : wm) * nk + kt];
+    w0 = wsc[(GATEUP ? 0 : wm * kRW / 128) * nk + kt];
     w1 = GATEUP ? wsc[nk + kt] : w0;
   };
   float sc[2][kN16];
@@ -338,7 +342,10 @@ void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
   __shared__ float scl[kActScales + kWScales];
   const TileItem it = decode_item(table[blockIdx.x]);
   if (it.g < 0) return;
-  if (it.narrow || it.tiny)        // a tiny tile's rows are a narrow tile's first rows
+  if (it.tiny)
+    tile_product_fp8<GATEUP, Tiny>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                   it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
+  else if (it.narrow)
     tile_product_fp8<GATEUP, Narrow>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
                                      it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
   else

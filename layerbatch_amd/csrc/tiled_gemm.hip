@@ -114,8 +114,9 @@ __device__ __forceinline__ int block_scan_1024(int v, int& excl, int* wsum) {
 }
 
 // Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
-// fastest; the W wide items come first, then the N narrow and tiny ones (both "narrow" below). XCD x owns the x-th contiguous
-// eighth of the wide items and of the narrow items, so items that share a token tile run on
+// fastest; the W wide items come first, then the N narrow and tiny ones (both "narrow" below).
+// XCD x owns the x-th contiguous eighth of the wide items and of the narrow items, so items
+// that share a token tile run on
 // one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
 // (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
 // (short, HBM-bound) items, so that the launch ends on short items, and its other narrow items
