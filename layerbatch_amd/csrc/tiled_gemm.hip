@@ -65,6 +65,10 @@ using Tiny = TileShape<4, 2, 1, 64, 3>;
 // 4 x 2 waves of 32 x 32 (128 x 64) with a ring small enough for two workgroups per CU
 using RouterShape = TileShape<4, 2, 1, 64, 3>;
 using RouterShape128 = TileShape<4, 1, 1, 64, 3>;
+// for batches that fill the chip with it: 2 x 4 waves of 128 x 32 (256 experts x 128 tokens),
+// which moves fewer operand bytes per flop than 64-token tiles
+using RouterShapeTall = TileShape<2, 4, 1, 64, 3>;
+constexpr int64_t kRouterTallMinWorkgroups = 256;
 constexpr int kLdsU4 = Wide::kRingU4 > Narrow::kRingU4 ? Wide::kRingU4 : Narrow::kRingU4;
 static_assert(Tiny::kRingU4 <= kLdsU4, "tiny ring exceeds the others");
 static_assert(kLdsU4 * 16 <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
@@ -116,12 +120,12 @@ __device__ __forceinline__ int block_scan_1024(int v, int& excl, int* wsum) {
 // Dispatch order of the GEMM items. Items are (token tile, weight tile) pairs, weight tile
 // fastest; the W wide items come first, then the N narrow and tiny ones (both "narrow" below).
 // XCD x owns the x-th contiguous eighth of the wide items and of the narrow items, so items
-// that share a token tile run on
-// one L2. Within an XCD the hardware hands out workgroups in order as CUs free up, so slot j
-// (= blockIdx / 8) is roughly a point in time: the XCD's last kTailSlots slots go to narrow
-// (short, HBM-bound) items, so that the launch ends on short items, and its other narrow items
-// are spread evenly between the wide (MFMA-bound) ones, so that weight streaming for small
-// experts overlaps MFMA work. Returns the item of workgroup b, or -1.
+// that share a token tile run on one L2. Within an XCD the hardware hands out workgroups in
+// order as CUs free up, so slot j (= blockIdx / 8) is roughly a point in time: the XCD's last
+// kTailSlots slots go to narrow (short, HBM-bound) items, so that the launch ends on short
+// items, and its other narrow items are spread evenly between the wide (MFMA-bound) ones, so
+// that weight streaming for small experts overlaps MFMA work. Returns the item of workgroup b,
+// or -1.
 constexpr int kTailSlots = 32;
 __device__ __forceinline__ int dispatch_item(int b, int W, int N) {
   const int x = b & 7, j = b >> 3;
@@ -633,6 +637,10 @@ hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, 
   gw.E = E;
   gw.H = H;
   if (E <= RouterShape128::kRows) return launch_router_shape<RouterShape128>(gw, x, T, logits, s);
+  const int64_t tall = (T + RouterShapeTall::kWT - 1) / RouterShapeTall::kWT *
+                       ((E + RouterShapeTall::kRows - 1) / RouterShapeTall::kRows);
+  if (tall >= kRouterTallMinWorkgroups)
+    return launch_router_shape<RouterShapeTall>(gw, x, T, logits, s);
   return launch_router_shape<RouterShape>(gw, x, T, logits, s);
 }
 

@@ -373,3 +373,20 @@ def test_experts_tile_class_boundaries(gpu, fp8):
     else:
         y_ref = om.experts(to_np(x)[rows], idx[rows], to_np(tw)[rows], wn["gate_up"], wn["down"])
         gc.check_output(to_np(y)[rows], y_ref, gc.TOL_BF16)
+
+
+# (E, T) per router tile shape: 128 experts x 64 tokens; 256 x 64; 256 x 128 once its tiles fill
+# the chip (T / 128 * ceil(E / 256) >= 256), also with a partial last expert tile
+@pytest.mark.parametrize("E,T", [(128, 1024), (512, 4096), (1024, 8192), (700, 11000)])
+def test_router_logits_tiled_shapes(gpu, E, T):
+    H = 512
+    g = torch.Generator().manual_seed(E + T)
+    wg = (torch.randn((E, H), generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    blk = Qwen3_5SparseMoeBlock(H, E, 2, 256, 0).to(device=gpu, dtype=torch.bfloat16)
+    with torch.no_grad():
+        blk.gate.weight.copy_(wg.to(gpu))
+    logits = blk.gate.logits(x.to(gpu))
+    torch.cuda.synchronize()
+    rows = np.unique(np.random.default_rng(E).choice(T, size=min(T, 1500), replace=False))
+    gc.check_logits(bf16_bits_of(logits)[rows], to_np(x)[rows], to_np(wg))
