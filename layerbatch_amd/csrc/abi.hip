@@ -178,7 +178,7 @@ struct StageEvents {
 static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx, int idx_bytes,
                            const void* topw, const float* sgate, int64_t T, void* y, void* ws,
                            const WsLayout& w, bool with_shared, hipStream_t s,
-                           StageEvents* ev = nullptr) {
+                           StageEvents* ev = nullptr, bool permuted = false) {
   StageEvents none{nullptr, 0, 0};
   if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
@@ -187,9 +187,10 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   int32_t* offsets = at<int32_t>(ws, w, R_OFFSETS);
   int32_t* perm_tok = at<int32_t>(ws, w, R_PERM_TOK);
   int32_t* inv = at<int32_t>(ws, w, R_INV);
-  LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
-                           at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
-                           at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
+  if (!permuted)
+    LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
+                             at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
+                             at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
   LBMOE_TRY(ev->mark(s));
   const GroupWeights gw = group_weights(L, with_shared, T);
   void* act = at<void>(ws, w, R_ACT);
@@ -336,6 +337,15 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
     LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
   }
   LBMOE_TRY(ev->mark(s));
+  // small batches route and permute in one kernel; profiled calls keep the two stages apart
+  if (!ev->events && route_perm_small_supported(T, L.top_k, L.num_experts)) {
+    LBMOE_TRY(launch_route_perm_small(
+        logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts, L.hidden_size, L.top_k,
+        static_cast<int32_t*>(idx), topw, sgate, at<int32_t>(ws, w, R_COUNTS),
+        at<int32_t>(ws, w, R_OFFSETS), at<int32_t>(ws, w, R_PERM_TOK),
+        at<int32_t>(ws, w, R_PERM_SLOT), at<int32_t>(ws, w, R_INV), s));
+    return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, true);
+  }
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,
                               L.hidden_size, L.top_k, idx, 4, topw, sgate, s));
   LBMOE_TRY(ev->mark(s));

@@ -12,6 +12,9 @@ namespace lbmoe {
 // Permutations of at most kPermSingle entries run in one workgroup; larger ones in chunks of
 // kPermChunk entries, one wave per chunk.
 constexpr int kPermSingle = 1024;
+// Batches up to this many tokens (4 for E > 128) route and permute in one kernel
+// (launch_route_perm_small).
+constexpr int64_t kSmallRouteTokens = 16;
 constexpr int kPermChunk = 256;
 
 inline int64_t perm_blocks(int64_t V) { return (V + kPermChunk - 1) / kPermChunk; }
@@ -91,6 +94,12 @@ hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, c
 hipError_t launch_route_topk(const void* logits, const float* bias, const void* x,
                              const void* w_sg, int64_t T, int E, int H, int k, void* idx,
                              int idx_bytes, void* topw, float* sgate, hipStream_t s);
+bool route_perm_small_supported(int64_t T, int k, int E);
+hipError_t launch_route_perm_small(const void* logits, const float* bias, const void* x,
+                                   const void* w_sg, int64_t T, int E, int H, int k, int32_t* idx,
+                                   void* topw, float* sgate, int32_t* counts, int32_t* offsets,
+                                   int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,
+                                   hipStream_t s);
 hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int E,
                           bool shared_rows, int32_t* counts, int32_t* offsets,
                           int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,

@@ -18,6 +18,7 @@
 // Entries whose expert id lies outside [0, E) are left out of every list and get inv = -1.
 #include "common.hpp"
 #include "internal.hpp"
+#include "route_token.hpp"
 
 namespace lbmoe {
 
@@ -195,11 +196,12 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
 // expert then turns the counts into per-virtual-wave prefixes (in v order) and a total, a block
 // scan of the totals gives the offsets, and every entry lands at offsets[e] + (entries of e in
 // earlier virtual waves) + rank.
+// The body, for a workgroup of kPermSingle threads that all call it (idx may point to LDS).
 template <int IB, int R, int EMAX>
-__global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int T, int k, int E,
-                                                           int nbits, int V, int32_t* counts,
-                                                           int32_t* offsets, int32_t* perm_tok,
-                                                           int32_t* perm_slot, int32_t* inv) {
+__device__ __forceinline__ void perm_single_body(const void* idx, int T, int k, int E, int nbits,
+                                                 int V, int32_t* counts, int32_t* offsets,
+                                                 int32_t* perm_tok, int32_t* perm_slot,
+                                                 int32_t* inv) {
   constexpr int kW = kPermSingle / kWave;
   constexpr int kVW = kW * R;            // virtual waves
   __shared__ int cnt[kVW][EMAX];         // per virtual wave and expert: count, then prefix
@@ -280,6 +282,34 @@ __global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int 
   }
 }
 
+template <int IB, int R, int EMAX>
+__global__ __launch_bounds__(kPermSingle) void perm_single(const void* idx, int T, int k, int E,
+                                                           int nbits, int V, int32_t* counts,
+                                                           int32_t* offsets, int32_t* perm_tok,
+                                                           int32_t* perm_slot, int32_t* inv) {
+  perm_single_body<IB, R, EMAX>(idx, T, k, E, nbits, V, counts, offsets, perm_tok, perm_slot, inv);
+}
+
+// Route and permutation of a small batch (route_perm_small_supported) in one workgroup: wave t selects token t's experts (route_token), the indices go
+// to LDS and to idx, and after a barrier the workgroup permutes them as perm_single does.
+// Saves a launch on the decode path of small batches.
+template <int EPL>
+__global__ __launch_bounds__(kPermSingle) void route_perm_small(
+    const uint16_t* __restrict__ logits, const float* __restrict__ bias,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w_sg, int T, int E, int H, int k,
+    int nbits, int32_t* __restrict__ idx, uint16_t* __restrict__ topw, float* __restrict__ sgate,
+    int32_t* counts, int32_t* offsets, int32_t* perm_tok, int32_t* perm_slot, int32_t* inv) {
+  __shared__ int32_t s_idx[kPermSingle];
+  const int wave = threadIdx.x / kWave;
+  if (wave < T)                                             // the same for the whole wave
+    route_token<EPL>(logits, bias, x, w_sg, wave, E, H, k, s_idx, 4, topw, sgate);
+  __syncthreads();
+  const int V = T * k;
+  if (static_cast<int>(threadIdx.x) < V) idx[threadIdx.x] = s_idx[threadIdx.x];
+  perm_single_body<4, 1, 1024>(s_idx, T, k, E, nbits, V, counts, offsets, perm_tok, perm_slot,
+                               inv);
+}
+
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t value) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) p[i] = value;
@@ -334,6 +364,34 @@ hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int 
                                base, lrank, s);
   return launch_permute_t<4>(idx, T, k, E, counts, offsets, perm_tok, perm_slot, inv, hist,
                              base, lrank, s);
+}
+
+// The fused kernel runs every token's selection on one CU: past 4 tokens that only pays while
+// each selection is short (E <= 128; at E = 512, T = 16 it was 2 us slower than two kernels).
+bool route_perm_small_supported(int64_t T, int k, int E) {
+  return T >= 1 && T <= (E <= 128 ? kSmallRouteTokens : 4) && T * k <= kPermSingle && E <= 1024;
+}
+
+hipError_t launch_route_perm_small(const void* logits, const float* bias, const void* x,
+                                   const void* w_sg, int64_t T, int E, int H, int k, int32_t* idx,
+                                   void* topw, float* sgate, int32_t* counts, int32_t* offsets,
+                                   int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,
+                                   hipStream_t s) {
+  const auto* lg = static_cast<const uint16_t*>(logits);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const auto* ws = static_cast<const uint16_t*>(w_sg);
+  auto* tw = static_cast<uint16_t*>(topw);
+  const int Ti = static_cast<int>(T), nbits = bits_for(E);
+#define LBMOE_ROUTE_PERM(EPL)                                                                  \
+  route_perm_small<EPL><<<1, kPermSingle, 0, s>>>(lg, bias, xx, ws, Ti, E, H, k, nbits, idx, tw, \
+                                                  sgate, counts, offsets, perm_tok, perm_slot, inv)
+  if (E <= 64) LBMOE_ROUTE_PERM(1);
+  else if (E <= 128) LBMOE_ROUTE_PERM(2);
+  else if (E <= 256) LBMOE_ROUTE_PERM(4);
+  else if (E <= 512) LBMOE_ROUTE_PERM(8);
+  else LBMOE_ROUTE_PERM(16);
+#undef LBMOE_ROUTE_PERM
+  return hipGetLastError();
 }
 
 }  // namespace lbmoe

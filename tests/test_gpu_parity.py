@@ -390,3 +390,17 @@ def test_router_logits_tiled_shapes(gpu, E, T):
     torch.cuda.synchronize()
     rows = np.unique(np.random.default_rng(E).choice(T, size=min(T, 1500), replace=False))
     gc.check_logits(bf16_bits_of(logits)[rows], to_np(x)[rows], to_np(wg))
+
+
+# small batches (up to 16 tokens for E <= 128, up to 4 otherwise) route and permute in one
+# kernel (one wave per token, then the one-workgroup permutation): every expert-count class of
+# the route, with and without a shared expert, and batches just past the limits
+@pytest.mark.parametrize("shape,T", [(MoEShape(512, 1024, 10, 256, 0), 4),
+                                     (MoEShape(512, 1024, 10, 256, 0), 16),
+                                     (MoEShape(512, 64, 16, 256, 256), 16),
+                                     (MoEShape(512, 200, 4, 256, 0), 1),
+                                     (MoEShape(512, 300, 8, 256, 256), 7),
+                                     (MoEShape(512, 128, 8, 256, 0), 13),
+                                     (MoEShape(512, 128, 8, 256, 0), 17)])
+def test_block_small_batch_route_permute(gpu, shape, T):
+    _run_and_check(shape, T, gpu, seed=13)
