@@ -106,7 +106,7 @@ def route(logits, k, bias=None):
 
 
 def route_by_prob(probs, k):
-    """The survey's canonical order on probabilities: (-p, expert index)."""
+    """Canonical order on probabilities: (-p, expert index), ties to the lower expert."""
     p = np.asarray(probs, dtype=np.float32)
     ar = np.broadcast_to(np.arange(p.shape[1]), p.shape)
     return np.lexsort((ar, -p), axis=-1)[:, :k].astype(np.int64)
