@@ -26,7 +26,7 @@ namespace f8t {
 // The LDS ring of 128-byte k-tiles (TileShape counts k-tiles in bf16 units: BK = 64).
 using Wide = TileShape<2, 4, 2, 64, 2>;
 using Narrow = TileShape<2, 4, 1, 64, 2>;
-using Tiny = TileShape<4, 2, 1, 64, 2>;       // 4 x 2 waves of 64 x 32: 64 tokens
+using Tiny = TileShape<4, 2, 1, 64, 3>;       // 4 x 2 waves of 64 x 32: 64 tokens
 constexpr int kRingU4 = Wide::kStages * Wide::kStageU4;
 static_assert(Narrow::kStages * Narrow::kStageU4 <= kRingU4, "narrow ring exceeds the wide one");
 static_assert(Tiny::kStages * Tiny::kStageU4 <= kRingU4, "tiny ring exceeds the wide one");
