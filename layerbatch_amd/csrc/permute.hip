@@ -10,8 +10,8 @@
 //             chunk's entries of the same expert (64-lane ballot matching on the expert
 //             bits), per-chunk histogram hist[e][chunk].
 //   per-expert one wave per expert: exclusive scan of hist[e][*] -> base[e][chunk], total[e].
-//   offsets   one workgroup: exclusive scan of the totals -> counts[e], offsets[e].
-//   scatter   one wave per chunk: pos = offsets[e] + base[e][chunk] + rank -> perm_tok,
+//   scatter   one wave per chunk: offsets[e] = exclusive scan of the totals (each workgroup
+//             scans them itself), pos = offsets[e] + base[e][chunk] + rank -> perm_tok,
 //             perm_slot, inv.
 // Up to 2 * kPermSingle entries (4 * kPermSingle for E <= 512), i.e. decode-sized batches, run
 // all of it in a single workgroup.
@@ -121,45 +121,16 @@ __global__ __launch_bounds__(64) void perm_expert_scan(const int32_t* __restrict
   if (lane == 63) totals[e] = incl;
 }
 
-// Exclusive scan of the E expert totals (one workgroup of 1024 threads, E <= 1024).
-__global__ __launch_bounds__(1024) void perm_offsets(const int32_t* __restrict__ totals, int E,
-                                                     int32_t* __restrict__ counts,
-                                                     int32_t* __restrict__ offsets) {
-  __shared__ int wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = tid < E ? totals[tid] : 0;
-  int incl = c;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < 16 ? wsum[lane] : 0;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const int y = __shfl_up(w, o, kWave);
-      if (lane >= o) w += y;
-    }
-    if (lane < 16) wsum[lane] = w;
-  }
-  __syncthreads();
-  const int excl = incl - c + (wave > 0 ? wsum[wave - 1] : 0);
-  if (tid < E) {
-    counts[tid] = c;
-    offsets[tid] = excl;
-  }
-  if (tid == 0) offsets[E] = wsum[15];
-}
-
+// Each workgroup first scans the E expert totals itself (exclusive, into LDS), so no separate
+// offsets pass runs between the per-expert scan and the scatter; workgroup 0 also stores the
+// offsets (E + 1 entries) for the later stages.
 template <int IB>
 __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k, int E, int V,
                                                    int nblk, const int32_t* base,
-                                                   const int32_t* offsets, const int32_t* lrank,
-                                                   int32_t* perm_tok, int32_t* perm_slot,
-                                                   int32_t* inv) {
+                                                   const int32_t* totals, int32_t* offsets,
+                                                   const int32_t* lrank, int32_t* perm_tok,
+                                                   int32_t* perm_slot, int32_t* inv) {
+  __shared__ int s_off[1024];
   const int lane = lane_id();
   const int b = blockIdx.x;
   // every expert id first, unconditionally (entries past V read entry V-1, V >= 1 here)
@@ -170,6 +141,25 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
     const int s = v / T;
     ev[r] = load_expert<IB>(idx, static_cast<int64_t>(v - s * T) * k + s);
   }
+  // lane l scans experts [l * per, (l + 1) * per), per <= 16 (E <= 1024)
+  const int per = (E + kWave - 1) / kWave;
+  const int lo = min(E, lane * per), hi = min(E, lo + per);
+  int local = 0;
+  for (int e = lo; e < hi; ++e) local += totals[e];
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  int run = incl - local;
+  for (int e = lo; e < hi; ++e) {
+    s_off[e] = run;
+    if (b == 0) offsets[e] = run;
+    run += totals[e];
+  }
+  if (b == 0 && lane == kWave - 1) offsets[E] = incl;
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int v = b * kPermChunk + r * kWave + lane;
@@ -182,7 +172,7 @@ __global__ __launch_bounds__(64) void perm_scatter(const void* idx, int T, int k
       inv[ts] = -1;
       continue;
     }
-    const int pos = offsets[e] + base[static_cast<int64_t>(e) * nblk + b] + lrank[v];
+    const int pos = s_off[e] + base[static_cast<int64_t>(e) * nblk + b] + lrank[v];
     perm_tok[pos] = t;
     perm_slot[pos] = s;
     inv[ts] = pos;
@@ -344,14 +334,13 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
   if (V <= kPermSingle) return single.template operator()<1, 1024>();
   if (V <= 2 * kPermSingle) return single.template operator()<2, 1024>();
   if (V <= 4 * kPermSingle && E <= 512) return single.template operator()<4, 512>();
-  // hist, base: E x nblk; lrank: V; the totals reuse the counts array until perm_offsets
+  // hist, base: E x nblk; lrank: V; the per-expert totals are the counts
   const int nblk = static_cast<int>(perm_blocks(V));
   perm_count<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist,
                                      lrank);
   perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
-  perm_offsets<<<1, 1024, 0, s>>>(counts, E, counts, offsets);
-  perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, offsets,
-                                       lrank, perm_tok, perm_slot, inv);
+  perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, counts,
+                                       offsets, lrank, perm_tok, perm_slot, inv);
   return hipGetLastError();
 }
 
