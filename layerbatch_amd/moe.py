@@ -56,6 +56,18 @@ def _require(t, name, dtype=torch.bfloat16, ndim=None):
         raise RuntimeError(f"{name} must be contiguous")
 
 
+def _require_shape(t, shape, name):
+    """The C ABI sees only pointers: a tensor of another shape would be read (or written) out
+    of bounds, so every size is checked here before any launch."""
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _require_width(x, H, name="hidden_states"):
+    if x.shape[1] != H:
+        raise RuntimeError(f"{name} has {x.shape[1]} channels, the layer's hidden_size is {H}")
+
+
 def _device_tensors(module):
     """Every tensor a module's kernels read: parameters and installed fp8 codes and scales."""
     for p in module.parameters():
@@ -105,13 +117,17 @@ class Qwen3_5TopKRouter(nn.Module):
         self.logit_bias = None
 
     def _layer(self):
+        _require(self.weight, "gate.weight", ndim=2)
         E, H = self.weight.shape
+        if E != self.num_experts:
+            raise RuntimeError(f"gate.weight has {E} rows, the router has {self.num_experts} experts")
         L = LbmoeLayer()
         L.hidden_size, L.num_experts, L.top_k = H, E, self.top_k
         L.moe_intermediate_size = 256           # routed-expert sizes are unused by the router
         L.gate_weight = self.weight.data_ptr()
         if self.logit_bias is not None:
             _require(self.logit_bias, "logit_bias", torch.float32, 1)
+            _require_shape(self.logit_bias, (E,), "logit_bias")
             L.logit_bias = self.logit_bias.data_ptr()
         return L
 
@@ -119,6 +135,7 @@ class Qwen3_5TopKRouter(nn.Module):
         """bf16 router logits [T, E] (the F.linear of qwen3_5.py:769)."""
         _require(hidden_states, "hidden_states", ndim=2)
         _require(self.weight, "gate.weight", ndim=2)
+        _require_width(hidden_states, self.weight.shape[1])
         _same_device(self, hidden_states.device)
         T = hidden_states.shape[0]
         out = torch.empty((T, self.num_experts), dtype=torch.bfloat16, device=hidden_states.device)
@@ -172,8 +189,11 @@ class Qwen3_5Experts(nn.Module):
             L.gate_up_scale = self.gate_up_scale.data_ptr()
             L.down_scale = self.down_scale.data_ptr()
         else:
+            E, H, I = self.num_experts, self.hidden_size, self.intermediate_size
             _require(self.gate_up_proj, "experts.gate_up_proj", ndim=3)
             _require(self.down_proj, "experts.down_proj", ndim=3)
+            _require_shape(self.gate_up_proj, (E, 2 * I, H), "experts.gate_up_proj")
+            _require_shape(self.down_proj, (E, H, I), "experts.down_proj")
             L.gate_up_proj = self.gate_up_proj.data_ptr()
             L.down_proj = self.down_proj.data_ptr()
 
@@ -181,6 +201,7 @@ class Qwen3_5Experts(nn.Module):
         _require(hidden_states, "hidden_states", ndim=2)
         _require(top_k_indices, "top_k_indices", None, 2)
         _require(top_k_weights, "top_k_weights", torch.bfloat16, 2)
+        _require_width(hidden_states, self.hidden_size)
         if top_k_indices.dtype not in (torch.int64, torch.int32):
             raise RuntimeError(f"top_k_indices must be int64 or int32, got {top_k_indices.dtype}")
         T, k = top_k_indices.shape
@@ -219,9 +240,11 @@ class Qwen3_5SharedExpertMLP(nn.Module):
             q = self.q
             return ([q[n][0].data_ptr() for n in ("gate", "up", "down")],
                     [q[n][1].data_ptr() for n in ("gate", "up", "down")])
-        for n, m in (("gate_proj", self.gate_proj), ("up_proj", self.up_proj),
-                     ("down_proj", self.down_proj)):
+        Is, H = self.gate_proj.weight.shape
+        for n, m, shape in (("gate_proj", self.gate_proj, (Is, H)), ("up_proj", self.up_proj, (Is, H)),
+                            ("down_proj", self.down_proj, (H, Is))):
             _require(m.weight, f"shared_expert.{n}.weight", ndim=2)
+            _require_shape(m.weight, shape, f"shared_expert.{n}.weight")
         return ([self.gate_proj.weight.data_ptr(), self.up_proj.weight.data_ptr(),
                  self.down_proj.weight.data_ptr()], [None, None, None])
 
@@ -236,6 +259,7 @@ class Qwen3_5SharedExpertMLP(nn.Module):
         _same_device(self, x.device)
         T, H = x.shape
         Is = self.gate_proj.weight.shape[0]
+        _require_width(x, self.gate_proj.weight.shape[1], "x")
         (g, u, d), (gs, us, ds) = self._ptrs()
         n = ctypes.c_size_t(0)
         check(lib().lbmoe_dense_mlp_workspace_size(H, Is, self.weight_dtype, T, ctypes.byref(n)),
@@ -283,13 +307,22 @@ class Qwen3_5SparseMoeBlock(nn.Module):
             self.shared_expert_gate = None
 
     def layer(self):
-        """The lbmoe_layer struct describing this block's parameters."""
+        """The lbmoe_layer struct describing this block's parameters (every tensor's shape is
+        checked against the block's sizes first)."""
         L = self.gate._layer()
+        H = self.experts.hidden_size
+        if L.hidden_size != H or L.num_experts != self.experts.num_experts:
+            raise RuntimeError(f"gate.weight {tuple(self.gate.weight.shape)} disagrees with the "
+                               f"experts' (num_experts, hidden_size) = "
+                               f"({self.experts.num_experts}, {H})")
         self.experts.fill_layer(L)
         L.top_k = self.gate.top_k
         if self.shared_expert is not None:
             self.shared_expert.fill_layer(L)
+            if self.shared_expert.gate_proj.weight.shape[1] != H:
+                raise RuntimeError("shared_expert weights disagree with the block's hidden_size")
             _require(self.shared_expert_gate.weight, "shared_expert_gate.weight", ndim=2)
+            _require_shape(self.shared_expert_gate.weight, (1, H), "shared_expert_gate.weight")
             L.shared_expert_gate = self.shared_expert_gate.weight.data_ptr()
             if self.shared_expert.weight_dtype != self.experts.weight_dtype:
                 raise RuntimeError("experts and shared expert must use the same weight dtype")
@@ -300,6 +333,7 @@ class Qwen3_5SparseMoeBlock(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, workspace: torch.Tensor = None):
         _require(hidden_states, "hidden_states", ndim=2)
+        _require_width(hidden_states, self.experts.hidden_size)
         _same_device(self, hidden_states.device)
         T = hidden_states.shape[0]
         L = self.layer()
@@ -325,6 +359,8 @@ class Qwen3_5SparseMoeBlock(nn.Module):
         _require(hidden_states, "hidden_states", ndim=2)
         _require(residual, "residual", ndim=2)
         _require(norm.weight, "norm.weight", ndim=1)
+        _require_width(hidden_states, self.experts.hidden_size)
+        _require_shape(norm.weight, (self.experts.hidden_size,), "norm.weight")
         if residual.shape != hidden_states.shape:
             raise RuntimeError("hidden_states and residual must have the same shape")
         if residual.device != hidden_states.device or norm.weight.device != hidden_states.device:

@@ -11,7 +11,7 @@ from layerbatch_amd.moe import Qwen3_5SparseMoeBlock
 from layerbatch_amd.synth import MoEShape, make_layer, make_x
 from oracle import moe as om
 from tests import gpu_checks as gc
-from tests.helpers import bf16_bits_of, layer_np, to_np
+from tests.helpers import bf16_bits_of, layer_np, scale_blocks_pow2, scale_groups_pow2, to_np
 from tests.test_gpu_parity import _block, _region
 
 pytestmark = pytest.mark.gpu
@@ -40,9 +40,14 @@ def _fp8_oracle(wn, q, xn, idx, topw, shared):
     return y
 
 
-def _run_fp8(shape, T, device, seed=0, sample=None):
+def _run_fp8(shape, T, device, seed=0, sample=None, patterned=False):
     w, g = make_layer(shape, seed=seed)
     x = make_x(g, T, shape.hidden_size)
+    if patterned:
+        # every weight block scale and activation group scale differs from its neighbours
+        w = {k_: (scale_blocks_pow2(v) if k_ in ("gate_up", "down", "sh_gate", "sh_up", "sh_down")
+                  else v) for k_, v in w.items()}
+        x = scale_groups_pow2(x)
     blk = _block(shape, {k_: v.to(device) for k_, v in w.items()}, device)
     blk.quantize_fp8_()
     xd = x.to(device)
@@ -76,6 +81,15 @@ def _run_fp8(shape, T, device, seed=0, sample=None):
     # and the fp8 layer stays close to the bf16 layer it approximates
     y_bf = gc.block_reference(xn[rows], wn, idx[rows], topw[rows], k, shared=True if shared else None)
     assert om.rel_err(to_np(y)[rows], y_bf) < 0.1
+    if patterned:
+        # the pattern makes scale indexing visible: the oracle itself, given each weight block
+        # its k-neighbour's scale, lands ten times the tolerance away
+        shifted = om.experts_fp8(xn[rows], idx[rows], topw[rows], q["wgu_q"],
+                                 np.roll(q["wgu_s"], 1, axis=-1), q["wd_q"],
+                                 np.roll(q["wd_s"], 1, axis=-1))
+        y_routed = om.experts_fp8(xn[rows], idx[rows], topw[rows], q["wgu_q"], q["wgu_s"],
+                                  q["wd_q"], q["wd_s"])
+        assert om.rel_err(shifted, y_routed) > 10 * gc.TOL_FP8
     return err
 
 
@@ -98,6 +112,15 @@ def test_fp8_block_shared(gpu):
 def test_fp8_block_prefill_tiled(gpu, T):
     """Prefill-sized batch: fp8 LDS-tiled GEMMs (shared expert included)."""
     _run_fp8(MoEShape(1024, 16, 2, 512, 256), T, gpu, seed=T, sample=64)
+
+
+# weight blocks scaled by 2^((i+j) mod 5) and activation groups by 2^((t+3g) mod 3), so that
+# reading a neighbouring block's or group's scale fails by far more than 3e-2: streaming GEMMs
+# (T = 1, 64), the LDS-tiled GEMMs (T = 700, several k-tiles in both GEMMs), shared expert
+# included; every row
+@pytest.mark.parametrize("T", [1, 64, 700])
+def test_fp8_block_scale_patterns(gpu, T):
+    _run_fp8(MoEShape(1024, 16, 2, 768, 256), T, gpu, seed=T + 40, patterned=True)
 
 
 def test_fp8_dense_mlp(gpu):

@@ -2,9 +2,11 @@
 
 Every routing decision is checked exactly: router logits on sampled rows against the exact dot
 products, selection on all rows against the oracle's selection from the GPU's own logits, and
-the whole permutation. The layer output is checked against the float64 oracle on sampled rows;
-the oracle only ever touches the experts those rows selected, which are copied off the GPU one
-at a time.
+the whole permutation. The layer output is checked against the float64 oracle on every row up
+to 256 tokens, and above that on at least 256 random rows plus every row of the tiles where
+indexing mistakes would show: the hottest expert's first and last 256-token tiles, and the last
+rows of experts whose remainders take a 64-token and a 128-token tile. The oracle only ever
+touches the experts those rows selected, which are copied off the GPU one at a time.
 """
 import numpy as np
 import pytest
@@ -36,7 +38,35 @@ class _Experts:
         return self._a
 
 
-def _run_full(shape, T, device, seed, zipf, sample, fp8=False):
+WIDE, NARROW, TINY = 256, 128, 64      # token-tile widths of the LDS-tiled GEMMs
+
+
+def tile_rows(counts, offsets, perm_tok):
+    """Tokens of the tiles where a tiling mistake would show first: the hottest expert's first
+    and last wide tiles (its last rows included), and the last rows of one expert whose
+    remainder after its wide tiles takes a tiny tile and of one whose remainder takes a narrow
+    tile (preferring experts that also have wide tiles)."""
+    counts = np.asarray(counts, np.int64)
+    pos = []
+
+    def tokens(e, lo, hi):
+        return perm_tok[offsets[e] + np.arange(lo, hi)]
+
+    hot = int(np.argmax(counts))
+    n = int(counts[hot])
+    if n:
+        pos.append(tokens(hot, 0, min(WIDE, n)))
+        pos.append(tokens(hot, max(0, (n - 1) // WIDE * WIDE - WIDE), n))
+    rem = counts % WIDE
+    for lo, hi in ((1, TINY), (TINY + 1, NARROW)):
+        cand = np.nonzero((rem >= lo) & (rem <= hi))[0]
+        if cand.size:
+            e = int(cand[np.argmax(counts[cand])])
+            pos.append(tokens(e, int(counts[e] - rem[e]), int(counts[e])))
+    return np.unique(np.concatenate(pos)) if pos else np.zeros(0, np.int64)
+
+
+def _run_full(shape, T, device, seed, zipf, sample=256, fp8=False):
     w, g = make_layer(shape, seed=seed, device=device)
     x = make_x(g, T, shape.hidden_size, device=device)
     blk = _block(shape, w, device)
@@ -48,23 +78,27 @@ def _run_full(shape, T, device, seed, zipf, sample, fp8=False):
     y = blk(x, workspace=ws)
     torch.cuda.synchronize()
     E, k = shape.num_experts, shape.top_k
-    rows = np.unique(np.random.default_rng(seed).choice(T, size=min(sample, T), replace=False))
     xn = to_np(x)
     logits = to_np(_region(blk, ws, T, "logits", torch.bfloat16, (T, E)))
-    wg = to_np(w["gate"])
-    gc.check_logits(bf16_bits_of(_region(blk, ws, T, "logits", torch.bfloat16, (T, E)))[rows],
-                    xn[rows], wg)
     bias = None if blk.gate.logit_bias is None else blk.gate.logit_bias.cpu().numpy()
     topw = _region(blk, ws, T, "topk_w", torch.bfloat16, (T, k))
     idx = to_np(_region(blk, ws, T, "topk_idx", torch.int32, (T, k)))
     _, idx_ref = gc.check_route(idx, bf16_bits_of(topw), logits, bias, k)
     V = T * k
-    gc.check_permutation(idx_ref, E,
-                         to_np(_region(blk, ws, T, "counts", torch.int32, (E,))),
-                         to_np(_region(blk, ws, T, "offsets", torch.int32, (E + 1,))),
-                         to_np(_region(blk, ws, T, "perm_tok", torch.int32, (V,))),
+    counts = to_np(_region(blk, ws, T, "counts", torch.int32, (E,)))
+    offsets = to_np(_region(blk, ws, T, "offsets", torch.int32, (E + 1,)))
+    perm_tok = to_np(_region(blk, ws, T, "perm_tok", torch.int32, (V,)))
+    gc.check_permutation(idx_ref, E, counts, offsets, perm_tok,
                          to_np(_region(blk, ws, T, "perm_slot", torch.int32, (V,))),
                          to_np(_region(blk, ws, T, "inv", torch.int32, (T, k))))
+    if T <= sample:
+        rows = np.arange(T)
+    else:
+        rand = np.random.default_rng(seed).choice(T, size=sample, replace=False)
+        rows = np.unique(np.concatenate([rand, tile_rows(counts, offsets, perm_tok)]))
+    print(f"  T={T}: logits and output checked on {rows.size} rows", flush=True)
+    gc.check_logits(bf16_bits_of(_region(blk, ws, T, "logits", torch.bfloat16, (T, E)))[rows],
+                    xn[rows], to_np(w["gate"]))
     tw = to_np(topw)[rows]
     shared = shape.shared_expert_intermediate_size > 0
     if fp8:
@@ -88,39 +122,39 @@ def _run_full(shape, T, device, seed, zipf, sample, fp8=False):
     return gc.check_output(to_np(y)[rows], y_ref, tol)
 
 
-@pytest.mark.parametrize("T", [128, 256])
+@pytest.mark.parametrize("T", [16, 64, 128, 256])
 def test_fullsize_decode_qwen3_30b(gpu, T):
-    """Qwen3-30B-A3B layer (H=2048, E=128, top-8, I=768), decode batches."""
-    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=1, zipf=False, sample=24)
+    """Qwen3-30B-A3B layer (H=2048, E=128, top-8, I=768), decode batches, every row."""
+    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=1, zipf=False)
 
 
 # either side of the kernel switches: one token tile (up to 8 tokens per expert) / two / the
 # LDS-tiled GEMMs (from 28), and the single-workgroup permutation (up to 4096 entries)
 @pytest.mark.parametrize("T", [1, 136, 448, 449, 513])
 def test_fullsize_qwen3_30b_path_boundaries(gpu, T):
-    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=T, zipf=False, sample=12)
+    _run_full(SHAPES["qwen3-30b-a3b"], T, gpu, seed=T, zipf=False)
 
 
 @pytest.mark.parametrize("T", [16, 1100])
 def test_fullsize_e512_streaming_shared_slices(gpu, T):
     """E=512 with the shared expert's token passes spread over extra workgroup rows (T=1100:
     streaming with two token tiles, 35 passes on 16 slices)."""
-    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=T, zipf=False, sample=12)
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=T, zipf=False)
 
 
 def test_fullsize_prefill_qwen3_30b_zipf(gpu):
     """The same layer at T=8192 with the Zipf(1.2) router bias: empty experts, a hot expert
     with thousands of tokens, wide and narrow tiles."""
-    _run_full(SHAPES["qwen3-30b-a3b"], 8192, gpu, seed=0, zipf=True, sample=24)
+    _run_full(SHAPES["qwen3-30b-a3b"], 8192, gpu, seed=0, zipf=True)
 
 
 @pytest.mark.parametrize("T", [128, 4096])
 def test_fullsize_e512_shared(gpu, T):
     """Qwen3-Next-style layer: H=2048, E=512, top-10, I=512, shared expert Is=512."""
-    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=2, zipf=False, sample=16)
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=2, zipf=False)
 
 
 @pytest.mark.parametrize("T", [128, 16384])
 def test_fullsize_e512_fp8(gpu, T):
     """The E=512 layer with e4m3 weights and activations (per-block fp32 scales)."""
-    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=3, zipf=False, sample=8, fp8=True)
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=3, zipf=False, fp8=True)

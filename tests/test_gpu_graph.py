@@ -1,11 +1,16 @@
 """The layer on a caller's stream and under HIP graph capture: every kernel goes to the stream
 it is handed, and the library itself never allocates, synchronises or records a memset, so a
 captured graph replays bit-identically to eager calls."""
+import numpy as np
 import pytest
 import torch
 
-from layerbatch_amd.synth import MoEShape, make_layer, make_x
-from tests.test_gpu_parity import _block
+from layerbatch_amd.synth import SHAPES, MoEShape, make_layer, make_x
+from oracle import moe as om
+from tests import gpu_checks as gc
+from tests.helpers import bf16_bits_of, to_np
+from tests.test_gpu_fullsize import _Experts
+from tests.test_gpu_parity import _block, _region
 
 pytestmark = pytest.mark.gpu
 
@@ -76,16 +81,22 @@ def test_repeated_calls_are_deterministic(gpu):
     assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
 
 
-def test_decode_bucket_graphs(gpu):
+# the toy layer at the engine's small buckets, and the Qwen3-30B-A3B layer up to 256; the
+# replays of the buckets named last are also checked against the float64 oracle
+@pytest.mark.parametrize("shape,buckets,checked", [
+    (SHAPE, [1, 2, 4, 8, 16, 32, 48, 64], [48]),
+    (SHAPES["qwen3-30b-a3b"], [1, 8, 16, 64, 128, 256], [128, 256])])
+def test_decode_bucket_graphs(gpu, shape, buckets, checked):
     """The engine's decode capture (model_runner.py:1463-1507): one graph per batch bucket,
     captured from the largest bucket down in a shared memory pool, all reading slices of one
     static input buffer whose rows past the live batch are zeros (padded rows are routed like
     real ones), and one workspace for all of them. Every bucket's replay matches an eager call
-    on the same slice bit for bit."""
-    buckets = [1, 2, 4, 8, 16, 32, 48, 64]
-    w, g = make_layer(SHAPE, seed=11)
-    blk = _block(SHAPE, {k: v.to(gpu) for k, v in w.items()}, gpu)
-    static_x = torch.zeros((max(buckets), SHAPE.hidden_size), dtype=torch.bfloat16, device=gpu)
+    on the same slice bit for bit; the checked buckets' replays also match the oracle: exact
+    selection from the replay's own logits, the output within 1e-2 on every row."""
+    H, E, k = shape.hidden_size, shape.num_experts, shape.top_k
+    w, g = make_layer(shape, seed=11, device=gpu)
+    blk = _block(shape, w, gpu)
+    static_x = torch.zeros((max(buckets), H), dtype=torch.bfloat16, device=gpu)
     outputs = torch.zeros_like(static_x)
     # one workspace, sized for the largest bucket, shared by every graph
     ws = torch.empty(blk.workspace_size(max(buckets)), dtype=torch.uint8, device=gpu)
@@ -101,11 +112,24 @@ def test_decode_bucket_graphs(gpu):
         torch.cuda.synchronize()
     for bs in buckets:
         live = max(1, bs - 1 - bs // 4)                          # a partly filled bucket
-        x = make_x(g, live, SHAPE.hidden_size).to(gpu)
+        x = make_x(g, live, H, device=gpu)
         static_x.zero_()
         static_x[:live] = x
         graphs[bs].replay()
         torch.cuda.synchronize()
+        if bs in checked:
+            print(f"bucket {bs}: replay against the oracle", flush=True)
+            logits = to_np(_region(blk, ws, bs, "logits", torch.bfloat16, (bs, E)))
+            topw = _region(blk, ws, bs, "topk_w", torch.bfloat16, (bs, k))
+            idx = to_np(_region(blk, ws, bs, "topk_idx", torch.int32, (bs, k)))
+            _, idx_ref = gc.check_route(idx, bf16_bits_of(topw), logits, None, k)
+            xn = to_np(static_x[:bs])
+            y_ref = om.experts(xn, idx_ref, to_np(topw), _Experts(w["gate_up"]), _Experts(w["down"]))
+            if shape.shared_expert_intermediate_size:
+                gsh = om.shared_gate(xn, to_np(w["sh_gate_w"])).astype(np.float64)
+                y_ref = y_ref + gsh[:, None] * om.shared_expert(
+                    xn, to_np(w["sh_gate"]), to_np(w["sh_up"]), to_np(w["sh_down"]))
+            gc.check_output(to_np(outputs[:bs]), y_ref, gc.TOL_BF16)
         y_e = blk(static_x[:bs].clone())
         torch.cuda.synchronize()
         assert torch.equal(outputs[:bs], y_e), f"bucket {bs} replay differs from the eager result"

@@ -11,7 +11,7 @@ from layerbatch_amd.synth import MoEShape, SHAPES, make_layer, make_x, zipf_bias
 from oracle import moe as om
 from oracle.codecs import bf16_bits
 from tests import gpu_checks as gc
-from tests.helpers import bf16_bits_of, layer_np, to_np
+from tests.helpers import bf16_bits_of, layer_np, scale_blocks_pow2, scale_groups_pow2, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -248,6 +248,38 @@ def test_host_checks_before_any_launch(gpu):
     y = blk(x, workspace=torch.empty(n, dtype=torch.uint8, device=gpu))   # the exact size works
     torch.cuda.synchronize()
     assert y.shape == x.shape
+    # sizes the C ABI cannot see: an input of another width, a norm weight, a router bias or a
+    # shared-expert weight of the wrong size
+    wide = make_x(g, 8, shape.hidden_size + 128).to(gpu)
+    with pytest.raises(RuntimeError, match="channels"):
+        blk(wide)
+    with pytest.raises(RuntimeError, match="channels"):
+        blk.experts(wide, torch.zeros((8, 2), dtype=torch.int64, device=gpu),
+                    torch.zeros((8, 2), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(RuntimeError, match="channels"):
+        blk.gate(wide)
+    with pytest.raises(RuntimeError, match="channels"):
+        blk.forward_norm(wide, wide, _Norm(torch.zeros(shape.hidden_size + 128, dtype=torch.bfloat16,
+                                                       device=gpu), 1e-6))
+    with pytest.raises(RuntimeError, match="norm.weight"):
+        blk.forward_norm(x, x, _Norm(torch.zeros(shape.hidden_size // 2, dtype=torch.bfloat16,
+                                                 device=gpu), 1e-6))
+    blk.gate.logit_bias = torch.zeros(shape.num_experts - 1, dtype=torch.float32, device=gpu)
+    with pytest.raises(RuntimeError, match="logit_bias"):
+        blk(x)
+    blk.gate.logit_bias = None
+    sh_shape = MoEShape(1024, 16, 2, 512, 256)
+    sw, _ = make_layer(sh_shape, seed=1)
+    sblk = _block(sh_shape, {k_: v.to(gpu) for k_, v in sw.items()}, gpu)
+    with torch.no_grad():
+        sblk.shared_expert.down_proj.weight = torch.nn.Parameter(
+            torch.zeros((1024, 128), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(RuntimeError, match="shared_expert.down_proj"):
+        sblk(x)
+    with pytest.raises(RuntimeError, match="shared_expert.down_proj"):
+        sblk.shared_expert(x)
+    with pytest.raises(RuntimeError, match="channels"):
+        sblk.shared_expert(wide)
 
 
 @pytest.mark.parametrize("T,E,k,levels,bias", [(300, 128, 8, 3, False), (257, 512, 10, 4, False),
@@ -351,12 +383,19 @@ def _boundary_routing(seed):
     return T, idx.astype(np.int64), tw
 
 
-@pytest.mark.parametrize("fp8", [False, True])
-def test_experts_tile_class_boundaries(gpu, fp8):
-    shape = MoEShape(512, len(TILE_BOUNDARY_COUNTS), 1, 256, 0)
+# H = 512, I = 256: gate_up 8 (bf16) / 4 (fp8) k-tiles, down 4 / 2; H = 1024, I = 768: 16 / 8
+# and 12 / 6, so that every ring refills several times in both GEMMs (the fp8 case with
+# patterned block and group scales)
+@pytest.mark.parametrize("fp8,H,I", [(False, 512, 256), (True, 512, 256), (False, 1024, 768),
+                                     (True, 1024, 768)])
+def test_experts_tile_class_boundaries(gpu, fp8, H, I):
+    shape = MoEShape(H, len(TILE_BOUNDARY_COUNTS), 1, I, 0)
     T, idx, tw = _boundary_routing(31)
     w, g = make_layer(shape, seed=12)
     x = make_x(g, T, shape.hidden_size)
+    if fp8 and H > 512:
+        w = {k_: (scale_blocks_pow2(v) if k_ in ("gate_up", "down") else v) for k_, v in w.items()}
+        x = scale_groups_pow2(x)
     blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
     if fp8:
         blk.quantize_fp8_()
