@@ -16,8 +16,10 @@
  *  - Scratch memory is caller-owned: size it with lbmoe_workspace_size and pass it in.
  *  - Every entry point returns an lbmoe_status; a negative value means nothing was
  *    enqueued (argument errors) or the launch failed. There is no fallback path.
- *  - No global mutable state: concurrent calls on different streams with different
- *    workspaces are independent.
+ *  - The library's only global state is set once per device and then read: the
+ *    architecture check and the address of lbmoe_forward_static's workspace. Concurrent calls
+ *    on different streams with different workspaces are independent; lbmoe_forward_static
+ *    calls on one device share one workspace (see there).
  */
 #ifndef LBMOE_H
 #define LBMOE_H
@@ -38,7 +40,9 @@ typedef enum lbmoe_status {
   LBMOE_ERR_DTYPE = -3,       /* unknown weight dtype / index width                 */
   LBMOE_ERR_WORKSPACE = -4,   /* workspace smaller than lbmoe_workspace_size        */
   LBMOE_ERR_DEVICE = -5,      /* current device is not gfx950 / no device           */
-  LBMOE_ERR_LAUNCH = -6       /* a kernel launch reported an error                  */
+  LBMOE_ERR_LAUNCH = -6,      /* a kernel launch reported an error                  */
+  LBMOE_ERR_STATIC_LIMIT = -7 /* lbmoe_forward_static: the call needs more workspace than
+                                 LBMOE_STATIC_WORKSPACE_BYTES                          */
 } lbmoe_status;
 
 typedef enum lbmoe_weight_dtype {
@@ -116,6 +120,24 @@ int32_t lbmoe_forward_norm(const lbmoe_layer* layer, const void* hidden, const v
                            const void* norm_weight, float eps, int64_t T, void* y,
                            void* residual_out, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* Bytes of the device workspace lbmoe_forward_static uses (one per GPU, held until the process
+ * ends). */
+#define LBMOE_STATIC_WORKSPACE_BYTES (64u << 20)
+
+/*
+ * lbmoe_forward without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace is a library-owned device array of
+ * LBMOE_STATIC_WORKSPACE_BYTES per GPU; calls needing more (lbmoe_workspace_size of the
+ * layer at T) return LBMOE_ERR_STATIC_LIMIT and enqueue nothing. The call allocates nothing
+ * (no hipMalloc, no hipFree). Every call on one GPU uses the same array: calls that overlap on
+ * one GPU (different streams, different host threads) race, and the array keeps the last
+ * call's intermediates (nothing in it needs to start at zero). Results are those of
+ * lbmoe_forward, bit for bit.
+ */
+int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
+                             void* stream);
 
 /* Number of events lbmoe_forward_profiled records. */
 #define LBMOE_PROFILE_EVENTS 7

@@ -14,6 +14,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblbmoe.so
 
 LBMOE_PROFILE_EVENTS = 7
 PROFILE_STAGES = ("router_logits", "route_topk", "permute", "gate_up", "down", "combine")
+LBMOE_STATIC_WORKSPACE_BYTES = 64 << 20
+LBMOE_ERR_STATIC_LIMIT = -7
 LBMOE_W_BF16 = 0
 LBMOE_W_FP8_E4M3 = 1
 
@@ -51,6 +53,7 @@ _SIGS = {
     "lbmoe_workspace_region": (_i32, [_PL, _i64, _i32, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "lbmoe_forward": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p]),
     "lbmoe_forward_profiled": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p, ctypes.POINTER(_p), _i32]),
+    "lbmoe_forward_static": (_i32, [_PL, _p, _i64, _p, _p]),
     "lbmoe_forward_norm": (_i32, [_PL, _p, _p, _p, ctypes.c_float, _i64, _p, _p, _p, _sz, _p]),
     "lbmoe_router_logits": (_i32, [_PL, _p, _i64, _p, _p]),
     "lbmoe_route": (_i32, [_PL, _p, _p, _i64, _p, _i32, _p, _p, _p]),

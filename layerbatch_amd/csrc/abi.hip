@@ -256,6 +256,9 @@ const char* lbmoe_status_string(int32_t status) {
     case LBMOE_ERR_WORKSPACE: return "workspace too small";
     case LBMOE_ERR_DEVICE: return "current device is not gfx950";
     case LBMOE_ERR_LAUNCH: return "kernel launch failed";
+    case LBMOE_ERR_STATIC_LIMIT:
+      return "call needs more workspace than the static workspace holds "
+             "(LBMOE_STATIC_WORKSPACE_BYTES)";
     default: return "unknown status";
   }
 }
