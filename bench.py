@@ -16,7 +16,8 @@ Printed: one JSON line. `value` is the layer's algorithmic HBM throughput in GB/
 calls). `roofline` describes the dominant kernel (gate_up), timed with HIP events recorded on
 the library's stream around that kernel in profiled calls; its `traffic` comes from the
 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary. `cpu_baseline` times the torch-CPU
-restatement of the reference's decode algorithm (dense gather + bmm) on the host's cores.
+restatement of the reference's decode algorithm (dense gather + bmm) on the host's cores; the
+prefill object and the E=512 entries carry their own (the per-expert loop for prefill).
 """
 import argparse
 import ctypes
@@ -186,31 +187,52 @@ def pmc_traffic(kernel):
 
 
 def cpu_baseline(blk, x, zipf, budget_s):
-    """The torch-CPU restatement of the reference path on this host's cores."""
+    """The torch-CPU restatement of the reference path on this host's cores: the algorithm the
+    reference picks for this batch (dense gather + bmm for decode, the per-expert loop for
+    prefill, qwen3_5.py:808-813), shared expert included, on the block's bf16 weights (a block
+    converted to fp8 keeps them; the reference has no fp8 path). One warmup, then the median of
+    up to 5 calls within budget_s."""
     import torch
     from oracle import torch_ref
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
-    wg = blk.gate.weight.detach().cpu()
-    wgu = blk.experts.gate_up_proj.detach().cpu()
-    wd = blk.experts.down_proj.detach().cpu()
-    bias = None if blk.gate.logit_bias is None else blk.gate.logit_bias.cpu()
+
+    def cpu(t):
+        return None if t is None else t.detach().cpu()
+
+    wg = cpu(blk.gate.weight)
+    wgu = cpu(blk.experts.gate_up_proj)
+    wd = cpu(blk.experts.down_proj)
+    sh = None
+    if blk.shared_expert is not None:
+        se = blk.shared_expert
+        sh = (cpu(se.gate_proj.weight), cpu(se.up_proj.weight), cpu(se.down_proj.weight),
+              cpu(blk.shared_expert_gate.weight))
+    bias = cpu(blk.gate.logit_bias)
     xc = x.cpu()
     algorithm = "sparse" if zipf or x.shape[0] > 512 else "dense"
     k = blk.gate.top_k
     times = []
     with torch.inference_mode():
         t0 = time.perf_counter()
-        torch_ref.block(xc, wg, wgu, wd, k, bias=bias, algorithm=algorithm)       # warmup
+        torch_ref.block(xc, wg, wgu, wd, k, bias=bias, sh=sh, algorithm=algorithm)   # warmup
         first = time.perf_counter() - t0
         n = max(1, min(5, int(budget_s / max(first, 1e-3))))
         for _ in range(n):
             t0 = time.perf_counter()
-            torch_ref.block(xc, wg, wgu, wd, k, bias=bias, algorithm=algorithm)
+            torch_ref.block(xc, wg, wgu, wd, k, bias=bias, sh=sh, algorithm=algorithm)
             times.append(time.perf_counter() - t0)
     times.sort()
     return {"us_per_call": times[len(times) // 2] * 1e6, "cores": ncores, "calls": len(times),
             "algorithm": algorithm}
+
+
+def cpu_entry(c, value, unit, what):
+    """cpu_baseline object of the JSON line from a cpu_baseline() result."""
+    return {"value": value, "unit": unit, "cores": c["cores"], "kind": "port",
+            "us_per_call": round(c["us_per_call"], 1),
+            "sample": f"{c['calls']} timed calls (median, after 1 warmup) of the torch-CPU "
+                      f"restatement of the reference's {c['algorithm']} algorithm, {what}"}
 
 
 def measure_wall(blks, x, steps, warmup):
@@ -287,7 +309,7 @@ def norm_config(name, shape, hid, res, nw, steps, dev, eps=1e-6):
             "us_per_call_torch_norm_then_block": round(us_torch, 1), "bound": "hbm"}
 
 
-def extra_configs(dev, steps, only=None):
+def extra_configs(dev, steps, only=None, cpu_budget_s=0.0):
     """The other configurations of the measurement plan, each at one GPU: the decode sweep of
     the headline layer, the Qwen3-Next-style E=512 layer with a shared expert, and its fp8
     variant. Every entry: back-to-back us per call and the algorithmic rate. only: run just
@@ -354,12 +376,25 @@ def extra_configs(dev, steps, only=None):
             if wanted(name):
                 n = steps if T <= 256 else max(3, steps // 5)
                 us, hit = measure_wall([blk], x, n, max(1, n // 5))
-                out.append(entry(name, shape, T, us, hit, 1 if fp8 else 2,
-                                 "mfma" if fp8 and T > 256 else "hbm"))
+                e = entry(name, shape, T, us, hit, 1 if fp8 else 2,
+                          "mfma" if fp8 and T > 256 else "hbm")
+                if cpu_budget_s > 0:
+                    # the reference has no fp8 path: its bf16 path on the same layer instead
+                    c = cpu_baseline(blk, x, False, cpu_budget_s)
+                    lb, lf, _, _ = work(shape, T, hit, 2)
+                    what = (f"the bf16 layer these fp8 weights were quantised from (the "
+                            f"reference has no fp8 path), T={T}, same inputs" if fp8 else
+                            f"the whole layer at the same T={T} on the same inputs")
+                    e["cpu_baseline"] = (cpu_entry(c, round(lf / (c["us_per_call"] * 1e-6) / 1e12, 4),
+                                                   "TFLOP/s", what) if T > 256 else
+                                         cpu_entry(c, round(lb / (c["us_per_call"] * 1e-6) / 1e9, 3),
+                                                   "GB/s", what))
+                out.append(e)
             del x
         del blk
         torch.cuda.empty_cache()
     return out
+
 
 
 def main():
@@ -387,12 +422,8 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         c = cpu_baseline(blk, x, False, args.cpu_budget_s)
-        cpu = {"value": round(lb / (c["us_per_call"] * 1e-6) / 1e9, 3), "unit": "GB/s",
-               "cores": c["cores"], "kind": "port",
-               "us_per_call": round(c["us_per_call"], 1),
-               "sample": f"{c['calls']} timed calls (median, after 1 warmup) of the torch-CPU "
-                         f"restatement of the reference's {c['algorithm']} decode algorithm at "
-                         f"the same T={args.T} on the same inputs"}
+        cpu = cpu_entry(c, round(lb / (c["us_per_call"] * 1e-6) / 1e9, 3), "GB/s",
+                        f"the whole layer at the same T={args.T} on the same inputs")
     del blk, x
     torch.cuda.empty_cache()
 
@@ -415,10 +446,18 @@ def main():
                          "unit": "TFLOP/s",
                          "frac": round(pgf / (pgu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
                          "algorithmic_flops_per_launch": pgf, "avg_launch_us": round(pgu, 1)},
+            "cpu_baseline": None,
         }
+        if not args.no_cpu_baseline:
+            c = cpu_baseline(pblk, px, True, args.cpu_budget_s)
+            prefill["cpu_baseline"] = cpu_entry(
+                c, round(plf / (c["us_per_call"] * 1e-6) / 1e12, 4), "TFLOP/s",
+                f"the whole layer at the same T={args.prefill_T} with the same Zipf(1.2) router "
+                f"bias on the same inputs")
         del pblk, px
 
-    extra = None if args.no_extra else extra_configs(dev, args.steps)
+    extra = None if args.no_extra else extra_configs(
+        dev, args.steps, cpu_budget_s=0.0 if args.no_cpu_baseline else args.cpu_budget_s / 2)
 
     if args.copy_probe_mib:
         n = args.copy_probe_mib << 18
