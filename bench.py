@@ -33,6 +33,7 @@ if ROOT not in sys.path:
 METRIC = ("MoE layer µs/call + TFLOP/s (or GB/s) & % roofline, decode T=128 / "
           "prefill T=8192")
 HBM_PEAK_GBS = 8000.0
+SETTLE_S = 0.3      # untimed calls ahead of every configuration after the headline one
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
 
@@ -117,7 +118,23 @@ def layer_inputs(shape, T, seed, zipf, device, fp8=False):
     return blk, x
 
 
-def measure(blk, x, steps, warmup, hip):
+def settle(call, warmup, settle_s):
+    """`warmup` untimed calls, then more until `settle_s` seconds of calls have run: the GPU's
+    clocks take tens of milliseconds of sustained work to ramp up from idle (a prefill call
+    runs ~25% slower over its first ~30 calls), so a configuration measured right after
+    another phase of the run (allocation, host work) is timed in its steady state."""
+    import torch
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(4):
+            call()
+        torch.cuda.synchronize()
+
+
+def measure(blk, x, steps, warmup, hip, settle_s=0.0):
     """Wall time per call over `steps` plain calls, then per-stage HIP-event times over
     `steps` profiled calls. Returns a dict of timings and routing statistics."""
     import torch
@@ -129,9 +146,7 @@ def measure(blk, x, steps, warmup, hip):
     lib = _lib.lib()
     stream = _lib.stream_of(x.device)
     args = (ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws), ws.numel(), stream)
-    for _ in range(warmup):
-        _lib.check(lib.lbmoe_forward(*args), "lbmoe_forward")
-    torch.cuda.synchronize()
+    settle(lambda: _lib.check(lib.lbmoe_forward(*args), "lbmoe_forward"), warmup, settle_s)
     t0 = time.perf_counter()
     for _ in range(steps):
         lib.lbmoe_forward(*args)
@@ -250,9 +265,9 @@ def measure_wall(blks, x, steps, warmup):
         ws = torch.empty(_lib.workspace_size(L, T), dtype=torch.uint8, device=x.device)
         calls.append((L, ws, (ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws),
                               ws.numel(), stream)))
-    for i in range(warmup):
-        _lib.check(lib.lbmoe_forward(*calls[i % len(calls)][2]), "lbmoe_forward")
-    torch.cuda.synchronize()
+    it = iter(range(1 << 62))
+    settle(lambda: _lib.check(lib.lbmoe_forward(*calls[next(it) % len(calls)][2]), "lbmoe_forward"),
+           warmup, SETTLE_S)
     t0 = time.perf_counter()
     for i in range(steps):
         lib.lbmoe_forward(*calls[i % len(calls)][2])
@@ -290,9 +305,7 @@ def norm_config(name, shape, hid, res, nw, steps, dev, eps=1e-6):
         xn.copy_((o * (1.0 + nw.float())).type_as(h))
 
     def timed(fn):
-        for _ in range(max(2, steps // 5)):
-            fn()
-        torch.cuda.synchronize()
+        settle(fn, max(2, steps // 5), SETTLE_S)
         t0 = time.perf_counter()
         for _ in range(steps):
             fn()
@@ -431,7 +444,7 @@ def main():
     if not args.no_prefill:
         pblk, px = layer_inputs(shape, args.prefill_T, 0, True, dev)
         steps = max(3, args.steps // 5)
-        p = measure(pblk, px, steps, max(1, args.warmup // 5), hip)
+        p = measure(pblk, px, steps, max(1, args.warmup // 5), hip, SETTLE_S)
         plb, plf, pgb, pgf = work(shape, args.prefill_T, p["hit_experts"])
         pgu = p["stage_us"]["gate_up"]
         prefill = {
