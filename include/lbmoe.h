@@ -147,7 +147,9 @@ int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T,
  * events[0..6] are caller-created hipEvent_t handles (passed as void*), recorded on `stream`
  * before the first kernel and after each stage: router logits, top-k routing, permutation,
  * gate_up + SiLU*mul, down projection, combine. hipEventElapsedTime between consecutive
- * events gives each stage's device time.
+ * events gives each stage's device time. Batches that lbmoe_forward routes and permutes in one
+ * kernel (up to 16 tokens for at most 128 experts, else up to 4) run it here too: its time is
+ * the routing stage's, and the permutation stage is empty.
  */
 int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                                void* workspace, size_t workspace_bytes, void* stream,

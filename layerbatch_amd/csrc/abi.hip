@@ -192,7 +192,9 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
                              at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
                              at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
   LBMOE_TRY(ev->mark(s));
-  const GroupWeights gw = group_weights(L, with_shared, T);
+  GroupWeights gw = group_weights(L, with_shared, T);
+  // the weight-streaming GEMMs give workgroups only to the at most T*k experts with tokens
+  if (T * k < E) gw.hit_rows = static_cast<int>(T * k);
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
   if (is_fp8(L)) {
@@ -340,13 +342,15 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
     LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
   }
   LBMOE_TRY(ev->mark(s));
-  // small batches route and permute in one kernel; profiled calls keep the two stages apart
-  if (!ev->events && route_perm_small_supported(T, L.top_k, L.num_experts)) {
+  // small batches route and permute in one kernel (profiled calls time it as the routing
+  // stage, their permutation stage then being empty)
+  if (route_perm_small_supported(T, L.top_k, L.num_experts)) {
     LBMOE_TRY(launch_route_perm_small(
         logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts, L.hidden_size, L.top_k,
         static_cast<int32_t*>(idx), topw, sgate, at<int32_t>(ws, w, R_COUNTS),
         at<int32_t>(ws, w, R_OFFSETS), at<int32_t>(ws, w, R_PERM_TOK),
         at<int32_t>(ws, w, R_PERM_SLOT), at<int32_t>(ws, w, R_INV), s));
+    LBMOE_TRY(ev->mark(s));
     return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, true);
   }
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,

@@ -210,8 +210,9 @@ __global__ __launch_bounds__(64) void gate_up_fp8_kernel(GroupWeights gw, const 
                                                          int T, int shared_extra, int act_ld,
                                                          uint16_t* __restrict__ act) {
   __shared__ u32x4 lds[(2 + TT) * 256];
-  const GroupSlice gs = group_slice(gw, shared_extra);
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
   const int g = gs.g;
+  if (g < 0) return;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
@@ -283,8 +284,9 @@ __global__ __launch_bounds__(64) void down_fp8_kernel(GroupWeights gw, const uin
                                                       const int32_t* __restrict__ offsets, int T,
                                                       int shared_extra, uint16_t* __restrict__ out) {
   __shared__ u32x4 lds[(2 + TT) * 256];
-  const GroupSlice gs = group_slice(gw, shared_extra);
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
   const int g = gs.g;
+  if (g < 0) return;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int n = shared ? T : counts[g];
@@ -360,7 +362,7 @@ hipError_t launch_gate_up_fp8(const GroupWeights& gw, const void* xq, const floa
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   return with_tt8(pick_tt8(gw, T, k), [&]<int TT>() {
     const int extra = shared_extra_rows(gw, T, 16 * TT);
-    gate_up_fp8_kernel<TT><<<dim3(Imax / 16, gw.groups + extra), 64, 0, s>>>(
+    gate_up_fp8_kernel<TT><<<dim3(Imax / 16, grid_groups(gw) + extra), 64, 0, s>>>(
         gw, static_cast<const uint8_t*>(xq), xs, counts, offsets, perm_tok, static_cast<int>(T),
         extra, act_ld, static_cast<uint16_t*>(act));
     return hipGetLastError();
@@ -372,7 +374,7 @@ hipError_t launch_down_fp8(const GroupWeights& gw, const void* actq, const float
                            int64_t T, int k, void* out, hipStream_t s) {
   return with_tt8(pick_tt8(gw, T, k), [&]<int TT>() {
     const int extra = shared_extra_rows(gw, T, 16 * TT);
-    down_fp8_kernel<TT><<<dim3(gw.H / 32, gw.groups + extra), 64, 0, s>>>(
+    down_fp8_kernel<TT><<<dim3(gw.H / 32, grid_groups(gw) + extra), 64, 0, s>>>(
         gw, static_cast<const uint8_t*>(actq), acts, act_ld, counts, offsets,
         static_cast<int>(T), extra, static_cast<uint16_t*>(out));
     return hipGetLastError();

@@ -57,22 +57,57 @@ struct GroupWeights {
   int E, H, I, Is;
   int g0, groups;
   int sh_row0;
+  // > 0: the weight-streaming GEMMs give routed experts only this many rows of workgroups, row
+  // y serving the y-th expert that received tokens (at most T*k of them exist), instead of one
+  // row per expert; for small batches most experts receive none.
+  int hit_rows;
 };
 
-// Grids of the weight-streaming GEMMs: row y < groups of workgroups serves group g0 + y. The
-// shared expert (the last group, when the launch has it) takes all T tokens, which one
-// workgroup would walk pass after pass; it gets shared_extra more rows of workgroups, and
-// slice s of its nslices takes passes s, s + nslices, ...
+// Grids of the weight-streaming GEMMs: the first rows of workgroups serve the routed groups,
+// row y group g0 + y (or, with hit_rows, the y-th routed expert with tokens). The shared
+// expert (the last group, when the launch has it) takes all T tokens, which one workgroup
+// would walk pass after pass; it gets shared_extra more rows of workgroups after the routed
+// ones, and slice s of its nslices takes passes s, s + nslices, ...
 struct GroupSlice {
-  int g, slice, nslices;
+  int g, slice, nslices;   // g < 0: no group for this row
 };
-__device__ __forceinline__ GroupSlice group_slice(const GroupWeights& gw, int shared_extra) {
-  const int y = blockIdx.y;
-  if (y < gw.groups) {
-    const int g = gw.g0 + y;
-    return {g, 0, g == gw.E ? shared_extra + 1 : 1};
+
+// The y-th expert (ascending) with counts[e] > 0 among E <= 1024, or -1; wave-uniform.
+__device__ __forceinline__ int nth_hit(const int32_t* __restrict__ counts, int E, int y) {
+  const int lane = threadIdx.x & 63;
+  int c[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) c[i] = counts[min(i * 64 + lane, E - 1)];   // all loads in flight
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint64_t m = __ballot(i * 64 + lane < E && c[i] > 0);
+    const int cnt = __popcll(m);
+    if (y < base + cnt) {
+      const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      const uint64_t sel = __ballot(((m >> lane) & 1) != 0 && below == y - base);
+      return i * 64 + __ffsll(static_cast<unsigned long long>(sel)) - 1;
+    }
+    base += cnt;
   }
-  return {gw.E, y - gw.groups + 1, shared_extra + 1};
+  return -1;
+}
+
+__host__ __device__ inline int routed_rows(const GroupWeights& gw) {
+  const int has_shared = gw.g0 + gw.groups > gw.E ? 1 : 0;
+  return gw.hit_rows > 0 ? gw.hit_rows : gw.groups - has_shared;
+}
+// Rows of workgroups of a weight-streaming GEMM launch before the shared expert's extra rows.
+inline int grid_groups(const GroupWeights& gw) {
+  return routed_rows(gw) + (gw.g0 + gw.groups > gw.E ? 1 : 0);
+}
+
+__device__ __forceinline__ GroupSlice group_slice(const GroupWeights& gw, int shared_extra,
+                                                  const int32_t* __restrict__ counts) {
+  const int y = blockIdx.y, rows = routed_rows(gw);
+  if (y < rows) return {gw.hit_rows > 0 ? nth_hit(counts, gw.E, y) : gw.g0 + y, 0, 1};
+  return {gw.E, y - rows, shared_extra + 1};
 }
 constexpr int kMaxSharedSlices = 16;
 // Extra workgroup rows for the shared expert at tokens_per_pass tokens per pass.

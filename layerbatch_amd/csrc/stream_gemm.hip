@@ -343,8 +343,9 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
     GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T,
     int shared_extra, int act_ld, uint16_t* __restrict__ act) {
-  const GroupSlice gs = group_slice(gw, shared_extra);
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
   const int g = gs.g;
+  if (g < 0) return;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
@@ -406,7 +407,7 @@ hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int3
   const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
   auto go = [&]<int TT>() {
     const int extra = shared_extra_rows(gw, T, 16 * TT);
-    const dim3 grid(Imax / 16, gw.groups + extra);
+    const dim3 grid(Imax / 16, grid_groups(gw) + extra);
     const SplitPlan plan = split_plan(gw.H / kKBlock, TT, false);
     return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
       gate_up_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(
@@ -430,8 +431,9 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
     GroupWeights gw, const uint16_t* __restrict__ act, int act_ld,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T,
     int shared_extra, int width, uint16_t* __restrict__ out) {
-  const GroupSlice gs = group_slice(gw, shared_extra);
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
   const int g = gs.g;
+  if (g < 0) return;
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   if (Ig != width) return;          // groups of another width run in their own launch
@@ -482,7 +484,7 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
   auto go = [&](int K) {
     auto launch = [&]<int TT>() {
       const int extra = shared_extra_rows(gw, T, 16 * TT);
-      const dim3 grid(gw.H / 32, gw.groups + extra);
+      const dim3 grid(gw.H / 32, grid_groups(gw) + extra);
       const SplitPlan plan = split_plan(K / kKBlock, TT, true);
       return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
         down_bf16_kernel<TT_, MAXB><<<grid, 64 * plan.waves, 0, s>>>(

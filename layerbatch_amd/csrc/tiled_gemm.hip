@@ -39,26 +39,10 @@
 
 namespace lbmoe {
 
-#ifndef LBMOE_TILE_BK
-#define LBMOE_TILE_BK 64
-#endif
-#ifndef LBMOE_TILE_STAGES
-#define LBMOE_TILE_STAGES 3
-#endif
-#ifndef LBMOE_TILE_BSTAGES
-#define LBMOE_TILE_BSTAGES 2
-#endif
-#ifndef LBMOE_NARROW_BK
-#define LBMOE_NARROW_BK 64
-#endif
-#ifndef LBMOE_NARROW_STAGES
-#define LBMOE_NARROW_STAGES 3
-#endif
-
-// wide: 2 x 4 waves of 128 x 64 (256 tokens), 3 weight + 2 token stages; narrow: 2 x 4 waves
-// of 128 x 32 (128 tokens), 3 stages of both
-using Wide = TileShape<2, 4, 2, LBMOE_TILE_BK, LBMOE_TILE_STAGES, LBMOE_TILE_BSTAGES>;
-using Narrow = TileShape<2, 4, 1, LBMOE_NARROW_BK, LBMOE_NARROW_STAGES>;
+// wide: 2 x 4 waves of 128 x 64 (256 tokens), 3 weight + 2 token stages of 64-k tiles; narrow:
+// 2 x 4 waves of 128 x 32 (128 tokens), 3 stages of both
+using Wide = TileShape<2, 4, 2, 64, 3, 2>;
+using Narrow = TileShape<2, 4, 1, 64, 3>;
 // tiny: 4 x 2 waves of 64 x 32 (64 tokens), for a group's last few rows
 using Tiny = TileShape<4, 2, 1, 64, 3>;
 // router logits: 4 x 2 waves of 64 x 32 (256 experts x 64 tokens); for at most 128 experts
@@ -249,7 +233,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   constexpr int kMT = S::kMT, kNT = S::kNT, kRW = S::kRW, kWavesM = S::kWavesM;
   constexpr int kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
   constexpr int kRowsPerLoad = S::kRowsPerLoad, kALoads = S::kALoads, kBLoads = S::kBLoads;
-  constexpr int kLoads = S::kLoads, kKSteps = S::kKSteps, kStageU4 = S::kStageU4;
+  constexpr int kLoads = S::kLoads, kKSteps = S::kKSteps;
   constexpr int kSwzShift = S::kSwzShift;
   constexpr int kRows = S::kRows;                  // weight rows of the tile
   static_assert(ROUTER || kRows == kWM, "expert GEMMs take kWM weight rows per tile");
