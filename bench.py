@@ -185,14 +185,16 @@ def work(shape, T, n_hit, wb=2):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_decode_qwen3-30b-a3b_T128_pmc_traffic.txt")
+PREFILL_TRAFFIC_FILE = os.path.join(ROOT, "profiles",
+                                    "moe_prefill_qwen3-30b-a3b_T8192_zipf_pmc_traffic.txt")
 
 
-def pmc_traffic(kernel):
-    """HBM bytes per dispatch of `kernel` at the default decode workload, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated against a copy kernel); None if the
-    summary is absent."""
+def pmc_traffic(kernel, path=TRAFFIC_FILE):
+    """HBM bytes per dispatch of `kernel` at the default workload, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (calibrated against a copy kernel); None if the summary is
+    absent."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith(kernel) and line[len(kernel)] in " <":
                     return int(line.split()[-1])
@@ -410,6 +412,19 @@ def extra_configs(dev, steps, only=None, cpu_budget_s=0.0):
 
 
 
+def copy_probe(mib, dev):
+    """A plain copy kernel (torch.neg, fp32) over `mib` MiB, 3 times: the calibration dispatch
+    for the FETCH_SIZE / WRITE_SIZE counters (reads and writes `mib` MiB each)."""
+    if not mib:
+        return
+    import torch
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -420,7 +435,9 @@ def main():
     from layerbatch_amd.synth import SHAPES
     dev = torch.device("cuda:0")
     if args.only_extra is not None:
-        print(json.dumps({"metric": METRIC, "extra": extra_configs(dev, args.steps, args.only_extra)}))
+        extra = extra_configs(dev, args.steps, args.only_extra)
+        copy_probe(args.copy_probe_mib, dev)
+        print(json.dumps({"metric": METRIC, "extra": extra}))
         return
     hip = HipEvents()
     shape = SHAPES[args.shape]
@@ -442,6 +459,7 @@ def main():
 
     prefill = None
     if not args.no_prefill:
+        default_prefill = args.shape == "qwen3-30b-a3b" and args.prefill_T == 8192
         pblk, px = layer_inputs(shape, args.prefill_T, 0, True, dev)
         steps = max(3, args.steps // 5)
         p = measure(pblk, px, steps, max(1, args.warmup // 5), hip, SETTLE_S)
@@ -458,7 +476,9 @@ def main():
                          "achieved": round(pgf / (pgu * 1e-6) / 1e12, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s",
                          "frac": round(pgf / (pgu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                         "algorithmic_flops_per_launch": pgf, "avg_launch_us": round(pgu, 1)},
+                         "algorithmic_flops_per_launch": pgf, "avg_launch_us": round(pgu, 1),
+                         "traffic": (pmc_traffic("tiled_kernel<1>", PREFILL_TRAFFIC_FILE)
+                                     if default_prefill else None)},
             "cpu_baseline": None,
         }
         if not args.no_cpu_baseline:
@@ -472,14 +492,7 @@ def main():
     extra = None if args.no_extra else extra_configs(
         dev, args.steps, cpu_budget_s=0.0 if args.no_cpu_baseline else args.cpu_budget_s / 2)
 
-    if args.copy_probe_mib:
-        n = args.copy_probe_mib << 18
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+    copy_probe(args.copy_probe_mib, dev)
 
     default_workload = args.shape == "qwen3-30b-a3b" and args.T == 128
     traffic = pmc_traffic("gate_up_bf16_kernel") if default_workload else None
