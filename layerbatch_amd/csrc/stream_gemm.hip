@@ -153,7 +153,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* __rest
 // Decode sizes. Workgroup = 8 waves on one 16-expert x 16-token tile, wave w taking k-blocks
 // [nkb*w/8, nkb*(w+1)/8) of K (at most MAXB of them), so that every load of the wave is issued
 // before the first MFMA; the eight partial sums are added in LDS in a fixed order and
-// rounded once. NORM: x is not read but formed from the residual add and RMSNorm of the
+// rounded once. MFMA c of a k-block takes its 32 k in the operand layout straight from
+// memory: lane (r, q) loads k = 32c + 8q .. +8 of row r, so the four lanes of a row cover one
+// 64-byte segment and a load instruction touches 16 segments. (With k = 32q + 8c every
+// instruction touched 64 segments, 16 bytes of each, and the texture-address unit, at about
+// one segment per cycle, bounded the kernel.) NORM: x is not read but formed from the residual add and RMSNorm of the
 // decoder layer (below): each wave computes h and x for its k-blocks of the 16 token rows,
 // the waves' sums of squares meet in LDS, and the workgroups of expert tile 0 also store h
 // and x. Both variants run the same MFMA chains, so their logits are identical.
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_logits_kernel(
       if (i >= nb) break;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int k = (kb0 + i) * kKBlock + 32 * q + 8 * c;
+        const int k = (kb0 + i) * kKBlock + 32 * c + 8 * q;
         a[i][c] = ld16_stream(wrow + k);
         b[i][c] = ld16(nm.residual + row + k);
         c2[i][c] = ld16(nm.hidden + row + k);
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_logits_kernel(
       if (i >= nb) break;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int k = (kb0 + i) * kKBlock + 32 * q + 8 * c;
+        const int k = (kb0 + i) * kKBlock + 32 * c + 8 * q;
         if (store) *reinterpret_cast<u32x4*>(nm.res_out + row + k) = b[i][c];
         b[i][c] = norm_bf8(b[i][c], nwv[i][c], rn);                                // b := x
         if (store) *reinterpret_cast<u32x4*>(nm.x_out + row + k) = b[i][c];
@@ -247,7 +251,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_logits_kernel(
         if (base + i >= nb) break;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const int k = (kb0 + base + i) * kKBlock + 32 * q + 8 * c;
+          const int k = (kb0 + base + i) * kKBlock + 32 * c + 8 * q;
           a[i][c] = ld16_stream(wrow + k);
           b[i][c] = ld16(x + row + k);
         }
