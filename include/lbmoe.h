@@ -149,7 +149,9 @@ int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T,
  * gate_up + SiLU*mul, down projection, combine. hipEventElapsedTime between consecutive
  * events gives each stage's device time. Batches that lbmoe_forward routes and permutes in one
  * kernel (up to 16 tokens for at most 128 experts, else up to 4) run it here too: its time is
- * the routing stage's, and the permutation stage is empty.
+ * the routing stage's, and the permutation stage is empty. bf16 batches of at most 4 tokens
+ * with T*top_k <= 64 route and permute inside the gate_up kernel: both of those stages are
+ * empty and the gate_up stage includes them.
  */
 int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                                void* workspace, size_t workspace_bytes, void* stream,

@@ -175,10 +175,13 @@ struct StageEvents {
   }
 };
 
+// rt: the batch's routing runs inside the gate_up kernel (launch_gate_up_bf16_routed), which
+// also writes the permutation; only for bf16 weights and the weight-streaming GEMMs.
 static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx, int idx_bytes,
                            const void* topw, const float* sgate, int64_t T, void* y, void* ws,
                            const WsLayout& w, bool with_shared, hipStream_t s,
-                           StageEvents* ev = nullptr, bool permuted = false) {
+                           StageEvents* ev = nullptr, bool permuted = false,
+                           const SmallRoute* rt = nullptr) {
   StageEvents none{nullptr, 0, 0};
   if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
@@ -224,6 +227,7 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     LBMOE_TRY(ev->mark(s));
     return LBMOE_OK;
   }
+  if (rt && use_tiled(gw, T, k)) return LBMOE_ERR_SHAPE;   // not reached (see forward_impl)
   if (use_tiled(gw, T, k)) {
     // prefill-sized batch: LDS-tiled MFMA GEMMs over a device-built token-tile list
     int32_t* tiles = at<int32_t>(ws, w, R_TILES);
@@ -233,7 +237,8 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_down_tiled(gw, act, Imax, tiles, max_tiles, T, out, s));
   } else {
-    LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
+    if (rt) LBMOE_TRY(launch_gate_up_bf16_routed(gw, x, *rt, T, Imax, act, s));
+    else LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, k, out, s));
   }
@@ -342,6 +347,19 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
     LBMOE_TRY(launch_router_logits(x, L.gate_weight, T, L.num_experts, L.hidden_size, logits, s));
   }
   LBMOE_TRY(ev->mark(s));
+  // the smallest bf16 batches route inside the gate_up kernel (profiled calls then have
+  // empty routing and permutation stages; T*k/E <= 4 tokens per expert never reaches the
+  // tiled GEMMs)
+  if (!is_fp8(L) && inline_route_supported(T, L.top_k, L.num_experts)) {
+    const SmallRoute rt{static_cast<const uint16_t*>(logits), L.logit_bias,
+                        static_cast<const uint16_t*>(L.shared_expert_gate), L.top_k,
+                        static_cast<int32_t*>(idx), static_cast<uint16_t*>(topw), sgate,
+                        at<int32_t>(ws, w, R_COUNTS), at<int32_t>(ws, w, R_OFFSETS),
+                        at<int32_t>(ws, w, R_PERM_TOK), at<int32_t>(ws, w, R_PERM_SLOT),
+                        at<int32_t>(ws, w, R_INV)};
+    LBMOE_TRY(ev->mark(s));
+    return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, true, &rt);
+  }
   // small batches route and permute in one kernel (profiled calls time it as the routing
   // stage, their permutation stage then being empty)
   if (route_perm_small_supported(T, L.top_k, L.num_experts)) {

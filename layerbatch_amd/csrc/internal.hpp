@@ -142,6 +142,32 @@ hipError_t launch_permute(const void* idx, int idx_bytes, int64_t T, int k, int 
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
                                int k, int act_ld, void* act, hipStream_t s);
+// Batches of at most kInlineRouteTokens tokens (and T*k <= kInlineRouteEntries) skip the
+// route and permutation kernels on the bf16 decode path: every gate_up workgroup selects the
+// batch's experts from the logits itself (launch_gate_up_bf16_routed) and derives its own
+// group's rows, and the workgroups of the first channel block store the routing outputs.
+constexpr int64_t kInlineRouteTokens = 4;
+constexpr int kInlineRouteEntries = 64;
+bool inline_route_supported(int64_t T, int k, int E);
+// What the routed gate_up launch reads and writes besides the GEMM operands: the route's
+// inputs (logits, the optional bias and shared-expert gate weight) and the outputs of the
+// route and permutation kernels it replaces.
+struct SmallRoute {
+  const uint16_t* logits;
+  const float* bias;
+  const uint16_t* w_sg;
+  int k;
+  int32_t* idx;
+  uint16_t* topw;
+  float* sgate;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* perm_tok;
+  int32_t* perm_slot;
+  int32_t* inv;
+};
+hipError_t launch_gate_up_bf16_routed(const GroupWeights& gw, const void* x, const SmallRoute& rt,
+                                      int64_t T, int act_ld, void* act, hipStream_t s);
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
                             const int32_t* counts, const int32_t* offsets, int64_t T, int k,
                             void* out, hipStream_t s);

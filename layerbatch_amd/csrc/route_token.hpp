@@ -36,8 +36,8 @@ __device__ __forceinline__ int wave_min_i32(int v) {
   return min(min(r0, r1), min(r2, r3));
 }
 
-// Token t's selection: idx_out[t*k + s] (idx_bytes 4 or 8), topw[t*k + s], sgate[t] (when not
-// null). Every lane of the wave must call it; it uses no LDS and no barrier.
+// Token t's selection: idx_out[t*k + s] (idx_bytes 4 or 8), topw[t*k + s] and sgate[t] (each
+// when not null). Every lane of the wave must call it; it uses no LDS and no barrier.
 template <int EPL>
 __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
                                             const float* __restrict__ bias,
@@ -131,7 +131,7 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
   const float psum = wave_sum(p);
   if (lane < k) {
     const int64_t o = static_cast<int64_t>(t) * k + lane;
-    topw[o] = static_cast<uint16_t>(f2bf(p / psum));
+    if (topw != nullptr) topw[o] = static_cast<uint16_t>(f2bf(p / psum));
     if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o] = my_e;
     else reinterpret_cast<int32_t*>(idx_out)[o] = my_e;
   }

@@ -25,6 +25,7 @@
 // Accumulator lane (r, q) holds rows 4q..4q+3 of column r.
 #include "common.hpp"
 #include "internal.hpp"
+#include "route_token.hpp"
 #include "split_k.hpp"
 
 namespace lbmoe {
@@ -341,22 +342,17 @@ static int pick_tt(const GroupWeights& gw, int64_t T, int k) {
 // ---- gate_up + SiLU*mul ------------------------------------------------------------------
 // Workgroup (channel block cb, group g): gate rows [16cb, 16cb+16) and the matching up rows of
 // expert g; act[row, 16cb + c] = bf16(silu(gate) * up) (chunk(2,-1) + silu*mul of
-// qwen3_5.py:835-836).
+// qwen3_5.py:835-836). Group g has n rows from row0 on; toks[p] is the token of its row p
+// (not read for the shared expert, whose row p is token p).
 template <int TT, int MAXB>
-__global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
-    GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T,
-    int shared_extra, int act_ld, uint16_t* __restrict__ act) {
-  const GroupSlice gs = group_slice(gw, shared_extra, counts);
-  const int g = gs.g;
-  if (g < 0) return;
+__device__ __forceinline__ void gate_up_group(const GroupWeights& gw, const uint16_t* __restrict__ x,
+                                              int g, int n, int row0, const int32_t* toks,
+                                              int slice, int nslices, int act_ld,
+                                              uint16_t* __restrict__ act) {
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
-  if (c0 >= Ig) return;
-  const int n = shared ? T : counts[g];
-  if (n == 0) return;
-  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  if (c0 >= Ig || n == 0) return;
   const int H = gw.H;
   const int W = blockDim.x >> 6;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -375,14 +371,14 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
                           wup + static_cast<int64_t>(c0) * H * 2};
   const uint32_t aoff = static_cast<uint32_t>((q * H + 8 * r) * 2);
   __shared__ u32x4 lds[split_lds_u4<TT>()];
-  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
+  for (int p0 = 16 * TT * slice; p0 < n; p0 += 16 * TT * nslices) {
     const uint16_t* bp[TT][4];
 #pragma unroll
     for (int j = 0; j < TT; ++j)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int p = min(p0 + 16 * j + 4 * u + q, n - 1);   // past n: a real row, not stored
-        const int tok = shared ? p : perm_tok[row0 + p];
+        const int tok = shared ? p : toks[p];
         bp[j][u] = x + static_cast<int64_t>(tok) * H + 8 * r;
       }
     f32x4 acc[2][TT];
@@ -405,6 +401,155 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
   }
 }
 
+template <int TT, int MAXB>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tok, int T,
+    int shared_extra, int act_ld, uint16_t* __restrict__ act) {
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
+  if (gs.g < 0) return;
+  const bool shared = gs.g == gw.E;
+  const int n = shared ? T : counts[gs.g];
+  const int row0 = shared ? gw.sh_row0 : offsets[gs.g];
+  gate_up_group<TT, MAXB>(gw, x, gs.g, n, row0, shared ? nullptr : perm_tok + row0, gs.slice,
+                          gs.nslices, act_ld, act);
+}
+
+// The routing of a batch of T <= kInlineRouteTokens tokens with T*k <= kInlineRouteEntries,
+// redone by every workgroup of the routed gate_up launch in place of the route and
+// permutation kernels: the selection of route_topk (route_token, one wave per token), then
+// this workgroup's group in the order the permutation builds (experts ascending, within an
+// expert slot-major: entry v = s*T + t; permute.hip). Returns the group of workgroup row
+// blockIdx.y (with hit_rows the y-th expert that received tokens; the shared expert after the
+// routed rows; -1 for none) with its row count n, first row row0 and tokens toks[0 .. n).
+// The workgroups of channel block 0 store their group's perm_tok, perm_slot and inv entries;
+// workgroup (0, 0) also idx, topw, sgate, counts and offsets, so the later kernels and the
+// workspace regions hold what the two kernels would have written.
+template <int EPL>
+__device__ __forceinline__ int inline_route(const GroupWeights& gw, const SmallRoute& rt,
+                                            const uint16_t* __restrict__ x, int T, int& n_out,
+                                            int& row0_out, int* toks) {
+  __shared__ int s_idx[kInlineRouteEntries];   // token-major: [t * k + s]
+  __shared__ int s_cnt[1024];                  // per expert (workgroup (0, 0) only)
+  __shared__ unsigned long long s_hit[16];     // experts with tokens, E <= 1024 bits
+  __shared__ int s_res[3];
+  const int E = gw.E, k = rt.k, V = T * k;
+  const int W = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+  if (lead)
+    for (int e = threadIdx.x; e < E; e += blockDim.x) s_cnt[e] = 0;
+  if (threadIdx.x < 16) s_hit[threadIdx.x] = 0ull;
+  for (int t = wv; t < T; t += W)                       // the same for the whole wave
+    route_token<EPL>(rt.logits, rt.bias, x, rt.w_sg, t, E, gw.H, k, s_idx, 4,
+                     lead ? rt.topw : nullptr, lead ? rt.sgate : nullptr);
+  __syncthreads();
+  // wave 0, lane v: entry v = s*T + t
+  const bool valid = wv == 0 && lane < V;
+  const int s = lane / T, t = lane - (lane / T) * T;
+  const int e = valid ? s_idx[t * k + s] : 0;
+  if (valid) {
+    atomicOr(&s_hit[e >> 6], 1ull << (e & 63));
+    if (lead) atomicAdd(&s_cnt[e], 1);
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int rows = routed_rows(gw), y = blockIdx.y;
+    int g = -1;
+    if (y >= rows) {
+      g = E;
+    } else if (gw.hit_rows == 0) {
+      g = gw.g0 + y;
+    } else {
+      // the y-th set bit of the hit mask: word by a prefix sum over 16 lanes, then the bit
+      const unsigned long long word = lane < 16 ? s_hit[lane] : 0ull;
+      const int c = __popcll(word);
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int u = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += u;
+      }
+      const uint64_t who = __ballot(lane < 16 && y >= incl - c && y < incl);
+      if (who != 0) {
+        const int wl = __builtin_ctzll(who);
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(word), wl);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(word >> 32), wl);
+        const unsigned long long wd = (static_cast<unsigned long long>(hi) << 32) | lo;
+        const int rank = y - (__builtin_amdgcn_readlane(incl, wl) - __popcll(wd));
+        const unsigned long long below = wd & ((1ull << lane) - 1ull);
+        const uint64_t sel = __ballot(((wd >> lane) & 1ull) != 0 && __popcll(below) == rank);
+        g = wl * 64 + __builtin_ctzll(sel);
+      }
+    }
+    int n = 0, row0 = 0;
+    if (g >= 0 && g < E) {
+      const uint64_t eq = __ballot(valid && e == g);
+      n = __popcll(eq);
+      row0 = __popcll(__ballot(valid && e < g));
+      if (valid && e == g) {
+        const int p = __popcll(eq & ((1ull << lane) - 1ull));
+        toks[p] = t;
+        if (blockIdx.x == 0) {
+          rt.perm_tok[row0 + p] = t;
+          rt.perm_slot[row0 + p] = s;
+          rt.inv[t * k + s] = row0 + p;
+        }
+      }
+    }
+    if (lead) {
+      if (valid) rt.idx[t * k + s] = e;
+      // counts and offsets of every expert: lane l scans experts [l * per, (l + 1) * per)
+      const int per = (E + kWave - 1) / kWave;
+      const int lo = min(E, lane * per), hi = min(E, lo + per);
+      int local = 0;
+      for (int e2 = lo; e2 < hi; ++e2) local += s_cnt[e2];
+      int incl = local;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int u = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += u;
+      }
+      int run = incl - local;
+      for (int e2 = lo; e2 < hi; ++e2) {
+        const int c2 = s_cnt[e2];
+        rt.counts[e2] = c2;
+        rt.offsets[e2] = run;
+        run += c2;
+      }
+      if (lane == kWave - 1) rt.offsets[E] = incl;
+    }
+    if (lane == 0) {
+      s_res[0] = g;
+      s_res[1] = n;
+      s_res[2] = row0;
+    }
+  }
+  __syncthreads();
+  n_out = s_res[1];
+  row0_out = s_res[2];
+  return s_res[0];
+}
+
+template <int MAXB, int EPL>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_routed_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ x, SmallRoute rt, int T, int shared_extra,
+    int act_ld, uint16_t* __restrict__ act) {
+  __shared__ int toks[kInlineRouteTokens];
+  int n, row0;
+  const int g = inline_route<EPL>(gw, rt, x, T, n, row0, toks);
+  if (g < 0) return;
+  int slice = 0, nslices = 1;
+  if (g == gw.E) {
+    slice = blockIdx.y - routed_rows(gw);
+    nslices = shared_extra + 1;
+    n = T;
+    row0 = gw.sh_row0;
+  }
+  gate_up_group<1, MAXB>(gw, x, g, n, row0, toks, slice, nslices, act_ld, act);
+}
+
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
                                const int32_t* offsets, const int32_t* perm_tok, int64_t T,
                                int k, int act_ld, void* act, hipStream_t s) {
@@ -425,6 +570,32 @@ hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int3
     case 2: return go.template operator()<2>();
     default: return go.template operator()<4>();
   }
+}
+
+bool inline_route_supported(int64_t T, int k, int E) {
+  return T >= 1 && T <= kInlineRouteTokens && T * k <= kInlineRouteEntries && E <= 1024;
+}
+
+hipError_t launch_gate_up_bf16_routed(const GroupWeights& gw, const void* x, const SmallRoute& rt,
+                                      int64_t T, int act_ld, void* act, hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const int extra = shared_extra_rows(gw, T, 16);
+  const dim3 grid(Imax / 16, grid_groups(gw) + extra);
+  const SplitPlan plan = split_plan(gw.H / kKBlock, 1, false);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* a = static_cast<uint16_t*>(act);
+  const int Ti = static_cast<int>(T);
+  return with_maxb<1>(plan, [&]<int TT_, int MAXB>() {
+#define LBMOE_ROUTED(EPL) \
+  gate_up_bf16_routed_kernel<MAXB, EPL><<<grid, 64 * plan.waves, 0, s>>>(gw, xx, rt, Ti, extra, act_ld, a)
+    if (gw.E <= 64) LBMOE_ROUTED(1);
+    else if (gw.E <= 128) LBMOE_ROUTED(2);
+    else if (gw.E <= 256) LBMOE_ROUTED(4);
+    else if (gw.E <= 512) LBMOE_ROUTED(8);
+    else LBMOE_ROUTED(16);
+#undef LBMOE_ROUTED
+    return hipGetLastError();
+  });
 }
 
 // ---- down projection ---------------------------------------------------------------------

@@ -432,9 +432,15 @@ def test_router_logits_tiled_shapes(gpu, E, T):
 
 
 # small batches (up to 16 tokens for E <= 128, up to 4 otherwise) route and permute in one
-# kernel (one wave per token, then the one-workgroup permutation): every expert-count class of
-# the route, with and without a shared expert, and batches just past the limits
+# kernel (one wave per token, then the one-workgroup permutation), and up to 4 tokens with
+# T*k <= 64 inside every gate_up workgroup instead (bf16): every expert-count class of the
+# route, with and without a shared expert, with the compact workgroup rows (T*k < E) and
+# without them, and batches just past the limits; the routing regions are checked too
 @pytest.mark.parametrize("shape,T", [(MoEShape(512, 1024, 10, 256, 0), 4),
+                                     (MoEShape(512, 128, 8, 256, 0), 2),
+                                     (MoEShape(512, 64, 16, 256, 256), 4),
+                                     (MoEShape(512, 16, 8, 256, 0), 2),
+                                     (MoEShape(512, 300, 8, 256, 256), 3),
                                      (MoEShape(512, 1024, 10, 256, 0), 16),
                                      (MoEShape(512, 64, 16, 256, 256), 16),
                                      (MoEShape(512, 200, 4, 256, 0), 1),
