@@ -240,6 +240,14 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     if (rt) LBMOE_TRY(launch_gate_up_bf16_routed(gw, x, *rt, T, Imax, act, s));
     else LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
     LBMOE_TRY(ev->mark(s));
+    if (idx_bytes == 4 && down_combine_small_supported(gw, T, k)) {
+      // one launch for the down GEMM and the combine (profiled: the combine stage is empty)
+      LBMOE_TRY(launch_down_combine_small(gw, act, Imax, static_cast<const int32_t*>(idx), inv,
+                                          topw, sgate, T, k, with_shared, y, s));
+      LBMOE_TRY(ev->mark(s));
+      LBMOE_TRY(ev->mark(s));
+      return LBMOE_OK;
+    }
     LBMOE_TRY(launch_down_bf16(gw, act, Imax, counts, offsets, T, k, out, s));
   }
   LBMOE_TRY(ev->mark(s));

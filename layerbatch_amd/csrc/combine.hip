@@ -69,6 +69,102 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   }
 }
 
+// ---- down projection + combine for the smallest batches -------------------------------------
+// At T <= kFusedDownTokens the down GEMM's rows are so few that its launch, and the combine's
+// after it, cost more than their memory traffic: one launch does both. Workgroup = kFusedCols
+// output columns h0 .. h0+7 for every token; wave w takes entries j = w, w + 8, ... (entry
+// t*k + s: token t's slot s, routed to expert idx[j], its act row inv[j]; entries T*k + t: the
+// shared expert's row of token t) and computes out[j, h0 + r] = act[row] . Wd_e[h0 + r] for
+// its 8 rows: lane (r, u) holds chunks u, u + 8, ... (16 bytes each) of weight row r and of the
+// act row, so a load instruction reads 8 rows x 128 contiguous bytes, all of an entry's loads
+// are in flight together, and the 8 lanes of a row meet in a butterfly sum. Each product is
+// rounded to bf16 as the down GEMM stores it, and the combine then runs from LDS exactly as
+// combine_kernel does (fp32 in slot order, then the gated shared term, one bf16 rounding).
+// MAXC: chunks per lane for the widest expert (I or Is = 64 * MAXC).
+constexpr int kFusedWaves = 8;
+template <int MAXC>
+__global__ __launch_bounds__(64 * kFusedWaves) void down_combine_small_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ act, int act_ld, const int32_t* __restrict__ idx,
+    const int32_t* __restrict__ inv, const uint16_t* __restrict__ topw,
+    const float* __restrict__ sgate, int T, int k, uint16_t* __restrict__ y) {
+  __shared__ float s_out[kFusedDownEntries][kFusedCols];
+  const int H = gw.H, h0 = blockIdx.x * kFusedCols;
+  const int lane = lane_id(), r = lane >> 3, u = lane & 7;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int V = T * k, nent = V + (sgate != nullptr ? T : 0);
+  for (int j = wv; j < nent; j += kFusedWaves) {           // the same for the whole wave
+    const bool sh = j >= V;
+    const int Ig = sh ? gw.Is : gw.I;
+    // a pair whose expert id was out of range (inv < 0) contributes nothing; its loads read
+    // expert 0's weights and act row 0
+    const int iv = sh ? 0 : inv[j];
+    const bool drop = iv < 0;
+    const int row = sh ? gw.sh_row0 + (j - V) : (drop ? 0 : iv);
+    const uint16_t* wbase = sh ? static_cast<const uint16_t*>(gw.sh_down)
+                               : static_cast<const uint16_t*>(gw.down) +
+                                     static_cast<int64_t>(drop ? 0 : idx[j]) * H * gw.I;
+    const uint16_t* wrow = wbase + static_cast<int64_t>(h0 + r) * Ig;
+    const uint16_t* arow = act + static_cast<int64_t>(row) * act_ld;
+    const int nch = Ig / 8;
+    // unconditional loads (chunks past the row re-read its last chunk and are not added)
+    u32x4 wq[MAXC], aq[MAXC];
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const int c = min(u + 8 * i, nch - 1);
+      wq[i] = ld16_stream(wrow + 8 * c);
+      aq[i] = ld16(arow + 8 * c);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      if (u + 8 * i >= nch) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc += bf_lo(wq[i][q]) * bf_lo(aq[i][q]);
+        acc += bf_hi(wq[i][q]) * bf_hi(aq[i][q]);
+      }
+    }
+    acc += __shfl_xor(acc, 1, kWave);
+    acc += __shfl_xor(acc, 2, kWave);
+    acc += __shfl_xor(acc, 4, kWave);
+    if (u == 0) s_out[j][r] = drop ? 0.f : round_bf(acc);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * kFusedCols; i += blockDim.x) {
+    const int t = i / kFusedCols, col = i - t * kFusedCols;
+    float a = 0.f;
+    for (int s = 0; s < k; ++s) a += bf2f(topw[t * k + s]) * s_out[t * k + s][col];
+    if (sgate != nullptr) a += sgate[t] * s_out[V + t][col];
+    y[static_cast<int64_t>(t) * H + h0 + col] = static_cast<uint16_t>(f2bf(a));
+  }
+}
+
+bool down_combine_small_supported(const GroupWeights& gw, int64_t T, int k) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  return T >= 1 && T <= kFusedDownTokens && T * k + T <= kFusedDownEntries &&
+         gw.H % kFusedCols == 0 && Imax <= 64 * 16 && gw.I % 64 == 0 && gw.Is % 64 == 0;
+}
+
+hipError_t launch_down_combine_small(const GroupWeights& gw, const void* act, int act_ld,
+                                     const int32_t* idx, const int32_t* inv, const void* topw,
+                                     const float* sgate, int64_t T, int k, bool shared, void* y,
+                                     hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  const dim3 grid(gw.H / kFusedCols);
+  const auto* a = static_cast<const uint16_t*>(act);
+  const auto* tw = static_cast<const uint16_t*>(topw);
+  const float* g = shared ? sgate : nullptr;
+  auto* yy = static_cast<uint16_t*>(y);
+  const int Ti = static_cast<int>(T);
+  if (Imax <= 512)
+    down_combine_small_kernel<8><<<grid, 64 * kFusedWaves, 0, s>>>(gw, a, act_ld, idx, inv, tw, g, Ti, k, yy);
+  else if (Imax <= 768)
+    down_combine_small_kernel<12><<<grid, 64 * kFusedWaves, 0, s>>>(gw, a, act_ld, idx, inv, tw, g, Ti, k, yy);
+  else
+    down_combine_small_kernel<16><<<grid, 64 * kFusedWaves, 0, s>>>(gw, a, act_ld, idx, inv, tw, g, Ti, k, yy);
+  return hipGetLastError();
+}
+
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared, void* y,
                           hipStream_t s) {

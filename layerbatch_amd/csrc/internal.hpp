@@ -171,6 +171,17 @@ hipError_t launch_gate_up_bf16_routed(const GroupWeights& gw, const void* x, con
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
                             const int32_t* counts, const int32_t* offsets, int64_t T, int k,
                             void* out, hipStream_t s);
+// Batches of at most kFusedDownTokens tokens (bf16, weight streaming) run the down GEMM and
+// the combine as one kernel (launch_down_combine_small); the expert_out region is then not
+// written. Columns per workgroup and the LDS bound on entries (T*k + T).
+constexpr int64_t kFusedDownTokens = 2;
+constexpr int kFusedCols = 8;
+constexpr int kFusedDownEntries = 66;
+bool down_combine_small_supported(const GroupWeights& gw, int64_t T, int k);
+hipError_t launch_down_combine_small(const GroupWeights& gw, const void* act, int act_ld,
+                                     const int32_t* idx, const int32_t* inv, const void* topw,
+                                     const float* sgate, int64_t T, int k, bool shared, void* y,
+                                     hipStream_t s);
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared,
                           void* y, hipStream_t s);

@@ -201,6 +201,25 @@ def test_router_module_returns_reference_types(gpu):
     gc.check_output(to_np(y), y_ref, gc.TOL_BF16)
 
 
+# The experts module at one and two tokens, where int32 indices take the fused down + combine
+# kernel (int64 ones the separate kernels), with expert ids outside [0, E): such pairs are
+# dropped (inv = -1) and add nothing, as expert-parallel callers rely on.
+@pytest.mark.parametrize("T,idx_dtype", [(1, torch.int32), (2, torch.int32), (2, torch.int64)])
+def test_experts_small_batch_dropped_pairs(gpu, T, idx_dtype):
+    shape = MoEShape(512, 16, 4, 256, 0)
+    w, g = make_layer(shape, seed=21, device="cpu")
+    x = make_x(g, T, shape.hidden_size)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    idx = np.array([[3, 15, -1, 7], [16, 3, 0, 9]][:T], dtype=np.int64)
+    tw = (torch.rand((T, 4), generator=g) + 0.1).to(torch.bfloat16)
+    y = blk.experts(x.to(gpu), torch.from_numpy(idx).to(idx_dtype).to(gpu), tw.to(gpu))
+    ok = (idx >= 0) & (idx < shape.num_experts)
+    wn = layer_np(w)
+    y_ref = om.experts(to_np(x), np.where(ok, idx, 0), np.where(ok, to_np(tw), 0.0),
+                       wn["gate_up"], wn["down"])
+    gc.check_output(to_np(y), y_ref, gc.TOL_BF16)
+
+
 def test_shared_expert_mlp_module(gpu):
     shape = MoEShape(1024, 8, 2, 128, 384)
     w, g = make_layer(shape, seed=4)
