@@ -96,8 +96,9 @@ int32_t lbmoe_workspace_size(const lbmoe_layer* layer, int64_t T, size_t* bytes)
  * 4 counts int32 [E+1], 5 offsets int32 [E+2], 6 perm_tok int32 [T*k+T],
  * 7 perm_slot int32 [T*k], 8 inv int32 [T,k], 9 act bf16 [T*k+T, max(I,Is)]
  * (not written by the fp8 prefill path, whose gate_up stores the quantised act directly),
- * 10 expert_out bf16 [T*k+T, H], 11 xn bf16 [T,H] (the block input lbmoe_forward_norm
- * computes). */
+ * 10 expert_out bf16 [T*k+T, H] (not written for bf16 batches of at most 4 tokens, whose
+ * down projection and combine run as one kernel), 11 xn bf16 [T,H] (the block input
+ * lbmoe_forward_norm computes). */
 int32_t lbmoe_workspace_region(const lbmoe_layer* layer, int64_t T, int32_t region,
                                size_t* offset, size_t* bytes);
 
@@ -151,7 +152,9 @@ int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T,
  * kernel (up to 16 tokens for at most 128 experts, else up to 4) run it here too: its time is
  * the routing stage's, and the permutation stage is empty. bf16 batches of at most 4 tokens
  * with T*top_k <= 64 route and permute inside the gate_up kernel: both of those stages are
- * empty and the gate_up stage includes them.
+ * empty and the gate_up stage includes them. bf16 batches of at most 4 tokens run the down
+ * projection and the combine as one kernel, timed as the down stage (the combine stage is
+ * empty).
  */
 int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                                void* workspace, size_t workspace_bytes, void* stream,

@@ -174,7 +174,7 @@ hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
 // Batches of at most kFusedDownTokens tokens (bf16, weight streaming) run the down GEMM and
 // the combine as one kernel (launch_down_combine_small); the expert_out region is then not
 // written. Columns per workgroup and the LDS bound on entries (T*k + T).
-constexpr int64_t kFusedDownTokens = 2;
+constexpr int64_t kFusedDownTokens = 4;
 constexpr int kFusedCols = 8;
 constexpr int kFusedDownEntries = 66;
 bool down_combine_small_supported(const GroupWeights& gw, int64_t T, int k);
