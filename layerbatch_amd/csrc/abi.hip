@@ -181,7 +181,7 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
                            const void* topw, const float* sgate, int64_t T, void* y, void* ws,
                            const WsLayout& w, bool with_shared, hipStream_t s,
                            StageEvents* ev = nullptr, bool permuted = false,
-                           const SmallRoute* rt = nullptr) {
+                           const SmallRoute* rt = nullptr, bool own_ids = false) {
   StageEvents none{nullptr, 0, 0};
   if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
@@ -190,14 +190,17 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   int32_t* offsets = at<int32_t>(ws, w, R_OFFSETS);
   int32_t* perm_tok = at<int32_t>(ws, w, R_PERM_TOK);
   int32_t* inv = at<int32_t>(ws, w, R_INV);
-  if (!permuted)
+  GroupWeights gw = group_weights(L, with_shared, T);
+  // the weight-streaming GEMMs give workgroups only to the at most T*k experts with tokens
+  if (T * k < E) gw.hit_rows = static_cast<int>(T * k);
+  // the route's own ids (all in [0, E)) can be permuted inside the bf16 decode gate_up kernel
+  const bool perm_in_gate_up = own_ids && !permuted && idx_bytes == 4 && !is_fp8(L) &&
+                               !use_tiled(gw, T, k) && gate_up_perm_supported(gw, T, k);
+  if (!permuted && !perm_in_gate_up)
     LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
                              at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
                              at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
   LBMOE_TRY(ev->mark(s));
-  GroupWeights gw = group_weights(L, with_shared, T);
-  // the weight-streaming GEMMs give workgroups only to the at most T*k experts with tokens
-  if (T * k < E) gw.hit_rows = static_cast<int>(T * k);
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
   if (is_fp8(L)) {
@@ -237,8 +240,15 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_down_tiled(gw, act, Imax, tiles, max_tiles, T, out, s));
   } else {
-    if (rt) LBMOE_TRY(launch_gate_up_bf16_routed(gw, x, *rt, T, Imax, act, s));
-    else LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
+    if (rt) {
+      LBMOE_TRY(launch_gate_up_bf16_routed(gw, x, *rt, T, Imax, act, s));
+    } else if (perm_in_gate_up) {
+      const PermOut po{counts, offsets, perm_tok, at<int32_t>(ws, w, R_PERM_SLOT), inv};
+      LBMOE_TRY(launch_gate_up_bf16_perm(gw, x, static_cast<const int32_t*>(idx), po, T, k,
+                                         Imax, act, s));
+    } else {
+      LBMOE_TRY(launch_gate_up_bf16(gw, x, counts, offsets, perm_tok, T, k, Imax, act, s));
+    }
     LBMOE_TRY(ev->mark(s));
     if (idx_bytes == 4 && down_combine_small_supported(gw, T, k)) {
       // one launch for the down GEMM and the combine (profiled: the combine stage is empty)
@@ -382,7 +392,7 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,
                               L.hidden_size, L.top_k, idx, 4, topw, sgate, s));
   LBMOE_TRY(ev->mark(s));
-  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev);
+  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, false, nullptr, true);
 }
 
 }  // namespace lbmoe

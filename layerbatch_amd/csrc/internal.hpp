@@ -168,6 +168,23 @@ struct SmallRoute {
 };
 hipError_t launch_gate_up_bf16_routed(const GroupWeights& gw, const void* x, const SmallRoute& rt,
                                       int64_t T, int act_ld, void* act, hipStream_t s);
+// Decode batches whose every expert can receive tokens (T*k >= E, so each routed workgroup row
+// is one expert) skip the permutation kernel: each gate_up workgroup derives its expert's rows
+// from the selected experts (launch_gate_up_bf16_perm), channel block 0 writes them out, and
+// workgroup (0, 0) the counts and offsets. At most kFusedPermTokens tokens; the expert ids must
+// lie in [0, E) (the route's own output).
+constexpr int64_t kFusedPermTokens = 256;
+struct PermOut {
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* perm_tok;
+  int32_t* perm_slot;
+  int32_t* inv;
+};
+bool gate_up_perm_supported(const GroupWeights& gw, int64_t T, int k);
+hipError_t launch_gate_up_bf16_perm(const GroupWeights& gw, const void* x, const int32_t* idx,
+                                    const PermOut& po, int64_t T, int k, int act_ld, void* act,
+                                    hipStream_t s);
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
                             const int32_t* counts, const int32_t* offsets, int64_t T, int k,
                             void* out, hipStream_t s);

@@ -415,6 +415,127 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
                           gs.nslices, act_ld, act);
 }
 
+// Rows of routed group g from the selected experts idx [T][k] (int32, every id in [0, E)), in
+// the order the permutation builds (within an expert slot-major: (s, t) ascending;
+// permute.hip): row count n, first row row0 and toks[p], the token of row p. Thread t takes
+// token t (T <= threads): it loads the token's k ids and finds the slot s_t holding g, if any
+// (a token selects an expert at most once). Its rank is then the tokens with g in a lower
+// slot plus the lower tokens with g in slot s_t: per slot one ballot per wave, the wave
+// counts through LDS. The workgroups of channel block 0 store the group's perm_tok,
+// perm_slot and inv entries, workgroup (0, 0) the counts and offsets of every expert (an LDS
+// histogram). Every thread of the workgroup must call it. KMAX >= k.
+template <int KMAX>
+__device__ __forceinline__ void group_rows(const int32_t* __restrict__ idx, int T, int k, int E,
+                                           int g, const PermOut& po, int& n, int& row0,
+                                           int* toks) {
+  __shared__ int s_hist[1024];
+  __shared__ int s_cnt[kSplitMaxWaves][KMAX + 1];     // per wave: tokens with g per slot, ids < g
+  const int bd = blockDim.x, tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
+  const int nw = bd >> 6;
+  const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+  if (lead)
+    for (int e = tid; e < E; e += bd) s_hist[e] = 0;
+  const int t = min(tid, T - 1);                         // threads past T re-read token T-1
+  int ev[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) ev[j] = idx[t * k + min(j, k - 1)];   // unconditional loads
+  if (lead) __syncthreads();                             // histogram cleared
+  const bool own = tid < T;
+  int slot = -1, lt = 0;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    const bool ok = own && j < k;
+    if (ok && ev[j] == g) slot = j;
+    lt += ok && ev[j] < g;
+    if (lead && ok) atomicAdd(&s_hist[ev[j]], 1);
+  }
+  uint64_t mine = 0;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j >= k) break;
+    const uint64_t m = __ballot(slot == j);
+    if (slot == j) mine = m;
+    if (lane == 0) s_cnt[wv][j] = __popcll(m);
+  }
+  const int wlt = wave_sum_i32(lt);
+  if (lane == 0) s_cnt[wv][KMAX] = wlt;
+  __syncthreads();
+  // lane j < k: slot j's tokens in all waves (col) and in the waves before this one (pre);
+  // lane KMAX: the ids below g
+  int col = 0, pre = 0;
+  if (lane < k || lane == KMAX) {
+    for (int w = 0; w < nw; ++w) {
+      const int c = s_cnt[w][lane];
+      col += c;
+      pre += w < wv ? c : 0;
+    }
+  }
+  row0 = __shfl(col, KMAX, kWave);
+  const int cin = lane < k ? col : 0;
+  int base = cin;                                        // inclusive prefix over the slots
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const int u = __shfl_up(base, o, kWave);
+    if (lane >= o) base += u;
+  }
+  n = __shfl(base, 15, kWave);
+  base -= cin;                                           // tokens with g in lower slots
+  const int sl = slot < 0 ? 0 : slot;
+  const int rank = __shfl(base, sl, kWave) + __shfl(pre, sl, kWave);
+  if (slot >= 0) {
+    const int p = rank + mask_rank(mine);
+    toks[p] = t;
+    if (blockIdx.x == 0) {
+      po.perm_tok[row0 + p] = t;
+      po.perm_slot[row0 + p] = slot;
+      po.inv[t * k + slot] = row0 + p;
+    }
+  }
+  if (lead) {
+    __syncthreads();                                     // histogram complete
+    if (wv == 0) {
+      // counts and offsets of every expert: lane l scans experts [l * per, (l + 1) * per)
+      const int per = (E + kWave - 1) / kWave;
+      const int lo = min(E, lane * per), hi = min(E, lo + per);
+      int local = 0;
+      for (int e = lo; e < hi; ++e) local += s_hist[e];
+      int run = local;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int u = __shfl_up(run, o, kWave);
+        if (lane >= o) run += u;
+      }
+      const int tot = run;
+      run -= local;
+      for (int e = lo; e < hi; ++e) {
+        const int c = s_hist[e];
+        po.counts[e] = c;
+        po.offsets[e] = run;
+        run += c;
+      }
+      if (lane == kWave - 1) po.offsets[E] = tot;
+    }
+  }
+  __syncthreads();                                       // toks complete
+}
+
+template <int TT, int MAXB, int KMAX>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_perm_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ idx, PermOut po,
+    int T, int k, int shared_extra, int act_ld, uint16_t* __restrict__ act) {
+  __shared__ int toks[kFusedPermTokens];
+  const GroupSlice gs = group_slice(gw, shared_extra, nullptr);   // hit_rows == 0
+  if (gs.g < 0) return;
+  int n, row0;
+  if (gs.g == gw.E) {
+    n = T;
+    row0 = gw.sh_row0;
+  } else {
+    group_rows<KMAX>(idx, T, k, gw.E, gs.g, po, n, row0, toks);
+  }
+  gate_up_group<TT, MAXB>(gw, x, gs.g, n, row0, toks, gs.slice, gs.nslices, act_ld, act);
+}
+
 // The routing of a batch of T <= kInlineRouteTokens tokens with T*k <= kInlineRouteEntries,
 // redone by every workgroup of the routed gate_up launch in place of the route and
 // permutation kernels: the selection of route_topk (route_token, one wave per token), then
@@ -596,6 +717,41 @@ hipError_t launch_gate_up_bf16_routed(const GroupWeights& gw, const void* x, con
 #undef LBMOE_ROUTED
     return hipGetLastError();
   });
+}
+
+bool gate_up_perm_supported(const GroupWeights& gw, int64_t T, int k) {
+  if (T < 1 || T > kFusedPermTokens || T * k < gw.E || gw.E > 1024 || gw.hit_rows != 0 || k > 16)
+    return false;
+  const SplitPlan plan = split_plan(gw.H / kKBlock, pick_tt(gw, T, k), false);
+  return T <= 64 * plan.waves;                           // one token per thread
+}
+
+hipError_t launch_gate_up_bf16_perm(const GroupWeights& gw, const void* x, const int32_t* idx,
+                                    const PermOut& po, int64_t T, int k, int act_ld, void* act,
+                                    hipStream_t s) {
+  const int Imax = gw.I > gw.Is ? gw.I : gw.Is;
+  auto go = [&]<int TT>() {
+    const int extra = shared_extra_rows(gw, T, 16 * TT);
+    const dim3 grid(Imax / 16, grid_groups(gw) + extra);
+    const SplitPlan plan = split_plan(gw.H / kKBlock, TT, false);
+    return with_maxb<TT>(plan, [&]<int TT_, int MAXB>() {
+      const auto* xx = static_cast<const uint16_t*>(x);
+      auto* a = static_cast<uint16_t*>(act);
+      const int Ti = static_cast<int>(T);
+      if (k <= 8)
+        gate_up_bf16_perm_kernel<TT_, MAXB, 8><<<grid, 64 * plan.waves, 0, s>>>(
+            gw, xx, idx, po, Ti, k, extra, act_ld, a);
+      else
+        gate_up_bf16_perm_kernel<TT_, MAXB, 16><<<grid, 64 * plan.waves, 0, s>>>(
+            gw, xx, idx, po, Ti, k, extra, act_ld, a);
+      return hipGetLastError();
+    });
+  };
+  switch (pick_tt(gw, T, k)) {
+    case 1: return go.template operator()<1>();
+    case 2: return go.template operator()<2>();
+    default: return go.template operator()<4>();
+  }
 }
 
 // ---- down projection ---------------------------------------------------------------------
