@@ -154,7 +154,8 @@ int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T,
  * with T*top_k <= 64 route and permute inside the gate_up kernel: both of those stages are
  * empty and the gate_up stage includes them. bf16 batches of at most 4 tokens run the down
  * projection and the combine as one kernel, timed as the down stage (the combine stage is
- * empty).
+ * empty). bf16 decode batches of at most 256 tokens with T*top_k >= E permute inside the
+ * gate_up kernel: the permutation stage is empty.
  */
 int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                                void* workspace, size_t workspace_bytes, void* stream,
