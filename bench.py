@@ -495,7 +495,8 @@ def main():
     copy_probe(args.copy_probe_mib, dev)
 
     default_workload = args.shape == "qwen3-30b-a3b" and args.T == 128
-    traffic = pmc_traffic("gate_up_bf16_kernel") if default_workload else None
+    # the decode gate_up kernel at T=128 (which also derives its expert's rows from the route)
+    traffic = pmc_traffic("gate_up_bf16_perm_kernel") if default_workload else None
 
     out = {
         "metric": METRIC, "value": round(layer_gbs, 2), "unit": "GB/s", "n_gpus": 1,
@@ -514,7 +515,7 @@ def main():
         "stage_note": ("stage_us: HIP events between the stages of lbmoe_forward_profiled calls "
                        "(one call at a time); us_per_call: back-to-back lbmoe_forward calls, which "
                        "run under the sustained power limit and so slower per stage"),
-        "roofline": {"kernel": "gate_up_bf16_kernel", "bound": "hbm", "achieved": round(gu_gbs, 1),
+        "roofline": {"kernel": "gate_up_bf16_perm_kernel", "bound": "hbm", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": gb,
                      "avg_launch_us": round(gu_us, 2)},
