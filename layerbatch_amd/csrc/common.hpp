@@ -46,10 +46,24 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
 }
 
+// Maximum over the 16 lanes of a DPP row (lanes 16j .. 16j+15): quad permutations, then the
+// half-row and row mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xb1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4e>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+  return v;
+}
+
 // Activation quantisation (per row and 128 channels): scale = amax / 448, 1 for an all-zero
 // group; code = e4m3(value / scale). One group is held by 16 consecutive lanes of a wave
-// (lanes 16j .. 16j+15), 8 channels per lane as 8 bf16 in v; every lane of the group must be
-// active. Returns the lane's 8 codes; s receives the group's scale.
+// (lanes 16j .. 16j+15, one DPP row), 8 channels per lane as 8 bf16 in v; every lane of the
+// group must be active. Returns the lane's 8 codes; s receives the group's scale.
 __device__ __forceinline__ float fp8_scale_of(float amax) { return amax > 0.f ? amax / 448.0f : 1.0f; }
 __device__ __forceinline__ u32x2 quant_group16(u32x4 v, float& s) {
   float x[8];
@@ -61,8 +75,7 @@ __device__ __forceinline__ u32x2 quant_group16(u32x4 v, float& s) {
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  amax = row16_max(amax);
   s = fp8_scale_of(amax);
   u32x2 c;
 #pragma unroll

@@ -315,17 +315,26 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   ring_barrier();
   if constexpr (GATEUP) {
     // 16 lanes per token: the group's amax, scale and codes (as quant_groups_kernel computes
-    // them from the stored bf16 act)
+    // them from the stored bf16 act). All of a thread's tokens at once, so that their
+    // independent chains (LDS read, row maximum, divisions) overlap; tokens past the group's
+    // rows are computed from whatever the staging area holds and not stored.
     uint8_t* q = static_cast<uint8_t*>(dst);
     const int sub = threadIdx.x & 15;
-    for (int r = threadIdx.x >> 4; r < kWT; r += kThreads / 16) {
-      const int p = r0 + r;
-      if (p >= n) break;                                    // uniform over the token's lanes
+    constexpr int kPer = kThreads / 16, kIters = kWT / kPer;
+    static_assert(kWT % kPer == 0, "tokens per pass divide the tile");
+    u32x4 v[kIters];
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) v[i] = lds[staged_slot<kCols>((threadIdx.x >> 4) + i * kPer, sub)];
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+      const int p = r0 + (threadIdx.x >> 4) + i * kPer;
       float sc;
-      const u32x2 c = quant_group16(lds[staged_slot<kCols>(r, sub)], sc);
-      const int64_t row = row0 + p;
-      *reinterpret_cast<u32x2*>(q + row * dst_ld + c0 + 8 * sub) = c;
-      if (sub == 0) dst_sc[row * (dst_ld / 128) + c0 / 128] = sc;
+      const u32x2 c = quant_group16(v[i], sc);
+      if (p < n) {
+        const int64_t row = row0 + p;
+        *reinterpret_cast<u32x2*>(q + row * dst_ld + c0 + 8 * sub) = c;
+        if (sub == 0) dst_sc[row * (dst_ld / 128) + c0 / 128] = sc;
+      }
     }
   } else {
     store_staged<kCols, kWT>(lds, static_cast<uint16_t*>(dst), dst_ld, row0, r0, n, c0);
