@@ -131,6 +131,14 @@ __host__ __device__ constexpr int64_t table_base(int max_tiles) {
   return (2 * static_cast<int64_t>(max_tiles) + kTileListTail + 3) / 4 * 4;
 }
 
+// Work queues of the persistent gate_up launch, behind both dispatch tables: 8 counters (one per
+// XCD, 64 ints apart so that they sit on different cache lines), then the 8 queue lengths.
+constexpr int kQueueInts = 8 * 64 + 8;
+__host__ __device__ inline int32_t* queue_base(int32_t* tiles, int max_tiles, int grid_gu,
+                                               int grid_dn) {
+  return tiles + table_base(max_tiles) + 4 * static_cast<int64_t>(grid_gu + grid_dn);
+}
+
 // One entry of a dispatch table: the work of workgroup b of a bf16 GEMM launch, read with a
 // single 16-byte load: {group | weight tile << 16 (-1: none), first row | narrow flag,
 // group's first row in the sorted rows, group's row count}. list: the tile list (2 ints per
@@ -207,6 +215,18 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     tiles[2 * max_tiles + 1] = n_wide;
   }
   if (grid_gu + grid_dn == 0) return;
+  if (tid < 8) {
+    // gate_up work queue of XCD x: its slots of the dispatch table (slot j = entry j * 8 + x)
+    // that dispatch_item fills, and a counter from zero
+    const int x = tid, n_wt = I > Is ? I / (kWM / 2) : Is / (kWM / 2);
+    const int W = n_wide * n_wt, N = (n_all - n_wide) * n_wt;
+    const int cw = (W + 7) >> 3, cn = (N + 7) >> 3;
+    const int nw = min(W, min(W, x * cw) + cw) - min(W, x * cw);
+    const int nn = min(N, min(N, x * cn) + cn) - min(N, x * cn);
+    int32_t* q = queue_base(tiles, max_tiles, grid_gu, grid_dn);
+    q[x * 64] = 0;
+    q[8 * 64 + x] = nw + nn;
+  }
   __syncthreads();                           // the list is complete (and visible to the block)
   const int* list = in_lds ? s_list : tiles;
   u32x4* tab = reinterpret_cast<u32x4*>(tiles + table_base(max_tiles));
@@ -223,12 +243,51 @@ enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 // Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
 // expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
 // src (down) / dst.
-template <int MODE, class S, int kLdsCap = kLdsU4>
+// Work queue of a persistent workgroup. XCD x's queue holds the dispatch-table entries
+// table[j * 8 + x], j < its length (the items a launch of one workgroup per entry would run on
+// that XCD, in the same order); its counter hands them out. A workgroup takes entries from its
+// home XCD's queue and, once that is empty, from the others in turn, so the last items of a
+// slow XCD spread over the chip.
+struct WorkQueue {
+  const u32x4* table;
+  int slots;       // table entries per XCD
+  int* q;          // counters q[x * 64], lengths q[8 * 64 + x]
+  int home;        // this workgroup's XCD
+  int tried;       // queues found empty so far
+  int own_len;     // length of the home queue
+};
+
+// Next entry (thread 0 only), synchronously: a queue whose counter has reached its length is
+// passed by with a load, otherwise an atomic takes an entry or finds the queue exhausted, so a
+// workgroup makes at most (entries taken + idle entries + 8) atomics.
+__device__ __forceinline__ u32x4 queue_fetch(WorkQueue& wq) {
+  while (wq.tried < 8) {
+    const int x = (wq.home + wq.tried) & 7;
+    int* cnt = wq.q + x * 64;
+    const int len = min(wq.q[8 * 64 + x], wq.slots);
+    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < len) {
+      const int j = atomicAdd(cnt, 1);
+      if (j < len) {
+        const u32x4 e = wq.table[j * 8 + x];
+        if (static_cast<int>(e[0]) >= 0) return e;
+        continue;                                  // an idle entry: the queue's next one
+      }
+    }
+    ++wq.tried;
+  }
+  return u32x4{0xffffffffu, 0u, 0u, 0u};
+}
+
+// PERSIST: called from the persistent kernel, which passes its work queue. The tile then claims
+// the next entry of the home queue after k-tile nk - 2's barrier, loads it at the start of the
+// epilogue, and leaves it (or, when the claim found nothing, a synchronously fetched entry) in
+// the ring's last 16 bytes, which no staged tile reaches.
+template <int MODE, class S, int kLdsCap = kLdsU4, bool PERSIST = false>
 __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint16_t* __restrict__ src,
                                              int src_ld, const int32_t* __restrict__ perm_tok,
                                              int g, int r0, int n, int row0, int wt,
                                              uint16_t* __restrict__ dst, int dst_ld,
-                                             u32x4* __restrict__ lds) {
+                                             u32x4* __restrict__ lds, WorkQueue* wq = nullptr) {
   constexpr bool GATEUP = MODE == kGateUp, ROUTER = MODE == kRouter;
   constexpr int kMT = S::kMT, kNT = S::kNT, kRW = S::kRW, kWavesM = S::kWavesM;
   constexpr int kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
@@ -244,9 +303,14 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   const int K = (GATEUP || ROUTER) ? H : Ig;
   const int c0 = wt * (GATEUP ? kRows / 2 : kRows);  // first channel / output column
 
-  const int lane = threadIdx.x & 63;
+  // In the persistent kernel's item loop the thread index goes through an empty asm, so the
+  // per-lane address arithmetic below is redone per item instead of being hoisted out of the
+  // loop and held in registers across the main loop (which spilled).
+  int tid = threadIdx.x;
+  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   // Wave index as a scalar: LDS destinations of the copies (M0) are then computed on the SALU.
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w % kWavesM, wn = w / kWavesM;
 
   // Direct global->LDS copies: wave copy i writes one contiguous 1 KB LDS block of
@@ -383,7 +447,8 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   // freed buffers take k-tile kt + kStages (2: both operands; 1: the asymmetric ring's token
   // operand only, whose ring runs one k-tile shorter). Specialised at compile time so that the loop body
   // has no branches around the MFMAs.
-  auto ktile = [&]<bool NEXT, int REFILL>(int kt) {
+  int claim = -1;      // PERSIST: home-queue slot claimed for the next item (-1: none)
+  auto ktile = [&]<bool NEXT, int REFILL, bool CLAIM = false>(int kt) {
 #pragma unroll
     for (int ks = 0; ks + 1 < kKSteps; ++ks) {
       read_frags(kt, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
@@ -409,6 +474,18 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
         if constexpr (REFILL >= 2) issue_a(kt % kStages, (kt + kStages) * kBK);
       } else {
         if constexpr (REFILL >= 2) issue(kt % kStages, (kt + kStages) * kBK);
+      }
+      if constexpr (CLAIM) {
+        // Every copy has landed (the wait above), so no ring wait counts the atomic. Through an
+        // address the compiler cannot prove uniform it stays a plain atomic whose result is
+        // waited for at its first use in the epilogue; the wave-level form it would otherwise
+        // take reads the result back right here.
+        if (threadIdx.x == 0 && wq->tried == 0) {
+          int* cnt = wq->q + wq->home * 64;
+          asm volatile("" : "+v"(cnt));
+          claim = __hip_atomic_fetch_add((__attribute__((address_space(1))) int*)cnt, 1,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
     mfma_all(fa[kl], fb[kl]);
@@ -440,7 +517,14 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   for (; kt + kStages < nk; ++kt) ktile.template operator()<true, 2>(kt);
   if constexpr (S::kAsym)
     for (; kt + S::kBStages < nk; ++kt) ktile.template operator()<true, 1>(kt);
-  for (; kt + 1 < nk; ++kt) ktile.template operator()<true, 0>(kt);
+  if constexpr (PERSIST) {
+    // k-tile nk - 2 claims the next item; outside the loop the claim's register is not carried
+    // around a loop edge, where the compiler copied it (and waited for the atomic) at once
+    for (; kt + 2 < nk; ++kt) ktile.template operator()<true, 0>(kt);
+    if (kt + 1 < nk) ktile.template operator()<true, 0, true>(kt++);
+  } else {
+    for (; kt + 1 < nk; ++kt) ktile.template operator()<true, 0>(kt);
+  }
   ktile.template operator()<false, 0>(kt);
 
   // Epilogue.
@@ -452,6 +536,17 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     constexpr int kCols = GATEUP ? kWM / 2 : kWM;            // output columns per tile
     static_assert(S::kWT * (kCols / 8) <= kLdsCap, "staged tile exceeds the LDS ring");
     ring_barrier();                                           // every wave is done with the ring
+    u32x4 next = {0xffffffffu, 0u, 0u, 0u};
+    if constexpr (PERSIST) {
+      static_assert(S::kWT * (kCols / 8) < kLdsCap, "the staged tile covers the next-item slot");
+      // the claimed entry's load goes out here and is used after the staging writes; the empty
+      // asm keeps the claim's first use (with the wait for the atomic) from moving up into the
+      // last k-tile
+      if (threadIdx.x == 0) {
+        asm volatile("" : "+v"(claim));
+        if (claim >= 0 && claim < wq->own_len) next = wq->table[claim * 8 + wq->home];
+      }
+    }
     char* st = reinterpret_cast<char*>(lds);
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
@@ -469,6 +564,17 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
           *reinterpret_cast<u32x2*>(st + staged_slot<kCols>(r, c / 8) * 16 + (c % 8) * 2) =
               u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         }
+    }
+    if constexpr (PERSIST) {
+      if (threadIdx.x == 0) {
+        if (static_cast<int>(next[0]) < 0) {
+          // no claim, a claim past the home queue's end (the queue is then empty), or an idle
+          // entry: fetch synchronously
+          if (claim >= wq->own_len) wq->tried = wq->tried > 1 ? wq->tried : 1;
+          next = queue_fetch(*wq);
+        }
+        lds[kLdsCap - 1] = next;
+      }
     }
     ring_barrier();
     store_staged<kCols, S::kWT>(lds, dst, dst_ld, row0, r0, n, c0);
@@ -532,6 +638,43 @@ void tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
                              dst_ld, lds);
 }
 
+// Persistent form of tiled_kernel: one workgroup per CU takes the dispatch-table entries from
+// the per-XCD work queues until they run dry. The hardware hands a launch's workgroups to an
+// XCD strictly in order, each to the next of its four shader engines in turn, so a CU that
+// finishes a short (HBM-bound) item waits until the workgroups ahead of the next one have found
+// CUs in their own shader engines; with wide items of ~53 us next to tiny ones of ~28 us, CUs of
+// the gate_up launch sat idle for 14% of its span. Taken from a queue, an item starts on
+// whichever CU of the XCD frees up first.
+template <int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tiled_persistent_kernel(GroupWeights gw, const uint16_t* __restrict__ src, int src_ld,
+                             const int32_t* __restrict__ perm_tok, const u32x4* __restrict__ table,
+                             int slots, int* __restrict__ q, uint16_t* __restrict__ dst,
+                             int dst_ld) {
+  __shared__ u32x4 lds[kLdsU4];
+  const int home = blockIdx.x & 7;                 // workgroup b runs on XCD b % 8
+  WorkQueue wq{table, slots, q, home, 0, 0};
+  if (threadIdx.x == 0) {
+    wq.own_len = min(q[8 * 64 + home], slots);
+    lds[kLdsU4 - 1] = queue_fetch(wq);
+  }
+  for (;;) {
+    ring_barrier();                    // the entry is in LDS, and the last tile's staging is read
+    const TileItem it = decode_item(lds[kLdsU4 - 1]);
+    ring_barrier();                    // every wave has the entry before the ring overwrites it
+    if (it.g < 0) break;               // the same for the whole workgroup
+    if (it.tiny)
+      tile_product<MODE, Tiny, kLdsU4, true>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n,
+                                             it.row0, it.wt, dst, dst_ld, lds, &wq);
+    else if (it.narrow)
+      tile_product<MODE, Narrow, kLdsU4, true>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n,
+                                               it.row0, it.wt, dst, dst_ld, lds, &wq);
+    else
+      tile_product<MODE, Wide, kLdsU4, true>(gw, src, src_ld, perm_tok, it.g, it.r0, it.n,
+                                             it.row0, it.wt, dst, dst_ld, lds, &wq);
+  }
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // Upper bound of the tile-list length: rows / wide full tiles, plus per group at most one
 // partial wide tile or (wide - narrow) / narrow narrow tiles.
@@ -558,7 +701,7 @@ static int down_wtiles(int H) { return H / kWM; }
 int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H) {
   const int64_t slots = item_grid(max_tiles, gate_up_wtiles(I, Is)) +
                         item_grid(max_tiles, down_wtiles(H));
-  return table_base(max_tiles) * 4 + slots * 16;
+  return table_base(max_tiles) * 4 + slots * 16 + kQueueInts * 4;       // + the work queues
 }
 
 int tiled_grid(const GroupWeights& gw, int max_tiles, bool gate_up) {
@@ -582,12 +725,42 @@ hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, con
   return hipGetLastError();
 }
 
+// CUs of the current device, rounded down to a multiple of 8 (every XCD the same number).
+static int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cus[kMaxDevices];             // per device, looked up once (0: not yet)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cus[dev] = n >= 8 ? n / 8 * 8 : 8;
+  }
+  return cus[dev];
+}
+
+// The persistent gate_up launch (one workgroup per CU) takes over from this many table entries
+// per CU: with fewer items per CU the in-order hardware dispatch leaves little idle and the
+// persistent loop's per-item queue work costs more than it saves (Qwen3-30B-A3B T=1024: 3.8
+// entries per CU, 2-5 us slower).
+constexpr int kPersistentMinEntriesPerCu = 6;
+
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s) {
-  tiled_kernel<kGateUp><<<tiled_grid(gw, max_tiles, true), kThreads, 0, s>>>(
-      gw, static_cast<const uint16_t*>(x), gw.H, perm_tok, tiled_table(gw, tiles, max_tiles, true),
-      static_cast<int>(T), static_cast<uint16_t*>(act), act_ld);
+  const int grid = tiled_grid(gw, max_tiles, true), cus = device_cus();
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const u32x4* table = tiled_table(gw, tiles, max_tiles, true);
+  auto* out = static_cast<uint16_t*>(act);
+  if (grid >= kPersistentMinEntriesPerCu * cus) {
+    int32_t* q = queue_base(const_cast<int32_t*>(tiles), max_tiles, grid,
+                            tiled_grid(gw, max_tiles, false));
+    tiled_persistent_kernel<kGateUp><<<cus, kThreads, 0, s>>>(gw, xx, gw.H, perm_tok, table,
+                                                              grid / 8, q, out, act_ld);
+  } else {
+    tiled_kernel<kGateUp><<<grid, kThreads, 0, s>>>(gw, xx, gw.H, perm_tok, table,
+                                                    static_cast<int>(T), out, act_ld);
+  }
   return hipGetLastError();
 }
 

@@ -119,6 +119,38 @@ def test_block_prefill_tiled_zipf(gpu, T):
     _run_and_check(shape, T, gpu, seed=7, bias=zipf_bias(g, 32), sample=96)
 
 
+def test_block_prefill_persistent_gate_up(gpu):
+    """A batch whose gate_up table has at least 6 entries per CU (H=1024, E=64, top-8, I=768,
+    T=8192: 1944 entries), so gate_up runs as the persistent work-queue kernel: wide, narrow and
+    tiny tiles, Zipf-skewed loads, and empty experts, whose queue entries are idle."""
+    shape = MoEShape(1024, 64, 8, 768, 0)
+    T, E, k, I = 8192, 64, 8, 768
+    g = torch.Generator().manual_seed(23)
+    bias = zipf_bias(g, E)
+    _run_and_check(shape, T, gpu, seed=13, bias=bias, sample=96)
+    # every row of the gate_up output (act, in expert-sorted order), so that an item the queues
+    # skipped or ran twice shows, against float32 products on the same device
+    w, gx = make_layer(shape, seed=13)
+    x = make_x(gx, T, shape.hidden_size).to(gpu)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    blk.gate.logit_bias = bias.to(gpu)
+    ws = torch.full((blk.workspace_size(T),), 255, dtype=torch.uint8, device=gpu)  # NaN act
+    blk(x, workspace=ws)
+    torch.cuda.synchronize()
+    offsets = _region(blk, ws, T, "offsets", torch.int32, (E + 1,)).cpu().tolist()
+    perm_tok = _region(blk, ws, T, "perm_tok", torch.int32, (T * k,)).long()
+    act = _region(blk, ws, T, "act", torch.bfloat16, (T * k, I)).float()
+    ref = torch.empty_like(act)
+    for e in range(E):
+        a, b = offsets[e], offsets[e + 1]
+        if b > a:
+            wt = w["gate_up"][e].to(gpu).float().t().contiguous()
+            h = x[perm_tok[a:b]].float() @ wt
+            ref[a:b] = torch.nn.functional.silu(h[:, :I]) * h[:, I:]
+    assert offsets[E] == T * k
+    gc.check_output(act.cpu().numpy(), ref.cpu().numpy(), gc.TOL_BF16)
+
+
 def test_block_prefill_tiled_shared(gpu):
     """Tiled GEMMs with a shared expert of a different width (Is != I)."""
     shape = MoEShape(512, 16, 2, 256, 384)
