@@ -155,7 +155,10 @@ int32_t lbmoe_forward_static(const lbmoe_layer* layer, const void* x, int64_t T,
  * empty and the gate_up stage includes them. bf16 batches of at most 4 tokens run the down
  * projection and the combine as one kernel, timed as the down stage (the combine stage is
  * empty). bf16 decode batches of at most 256 tokens with T*top_k >= E permute inside the
- * gate_up kernel: the permutation stage is empty.
+ * gate_up kernel: the permutation stage is empty. Prefill batches (from 1024 tokens, with
+ * the LDS-tiled expert GEMMs) of at most 128 experts and top_k <= 16 select the experts inside
+ * the router kernel: the routing stage is empty, and the permutation stage also builds the
+ * GEMMs' tile list (otherwise launched with gate_up).
  */
 int32_t lbmoe_forward_profiled(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                                void* workspace, size_t workspace_bytes, void* stream,

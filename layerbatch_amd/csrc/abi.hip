@@ -19,7 +19,8 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
   const int64_t E = L.num_experts, k = L.top_k, H = L.hidden_size;
   const int64_t I = L.moe_intermediate_size, Is = L.shared_intermediate_size;
   const int64_t V = T * k, Vs = V + (Is > 0 ? T : 0), Imax = std::max(I, Is);
-  const int64_t nblk = perm_blocks(V);
+  // count chunks: kPermChunk entries (launch_permute) or slot x 64-token block (router_route)
+  const int64_t nblk = std::max(perm_blocks(V), router_route_chunks(T, static_cast<int>(k)));
   WsLayout w{};
   w.bytes[R_LOGITS] = T * E * 2;
   w.bytes[R_IDX] = V * 4;
@@ -177,11 +178,14 @@ struct StageEvents {
 
 // rt: the batch's routing runs inside the gate_up kernel (launch_gate_up_bf16_routed), which
 // also writes the permutation; only for bf16 weights and the weight-streaming GEMMs.
+// chunked: the route came from launch_router_route, whose per-chunk counts (R_HIST, R_LRANK)
+// the permutation finishes (scan, then scatter with the tile list).
 static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx, int idx_bytes,
                            const void* topw, const float* sgate, int64_t T, void* y, void* ws,
                            const WsLayout& w, bool with_shared, hipStream_t s,
                            StageEvents* ev = nullptr, bool permuted = false,
-                           const SmallRoute* rt = nullptr, bool own_ids = false) {
+                           const SmallRoute* rt = nullptr, bool own_ids = false,
+                           bool chunked = false) {
   StageEvents none{nullptr, 0, 0};
   if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
@@ -196,10 +200,23 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   // the route's own ids (all in [0, E)) can be permuted inside the bf16 decode gate_up kernel
   const bool perm_in_gate_up = own_ids && !permuted && idx_bytes == 4 && !is_fp8(L) &&
                                !use_tiled(gw, T, k) && gate_up_perm_supported(gw, T, k);
-  if (!permuted && !perm_in_gate_up)
+  int32_t* tiles = at<int32_t>(ws, w, R_TILES);
+  const int max_tiles = tiled_max_tiles(T * k + (with_shared ? T : 0), gw.groups);
+  bool tiles_built = false;
+  if (chunked) {
+    int32_t* base = at<int32_t>(ws, w, R_BASE);
+    LBMOE_TRY(launch_perm_scan(at<int32_t>(ws, w, R_HIST),
+                               static_cast<int>(router_route_chunks(T, k)), E, base, counts, s));
+    LBMOE_TRY(launch_scatter_build(static_cast<const int32_t*>(idx), T, k, base, counts,
+                                   at<int32_t>(ws, w, R_LRANK), offsets, perm_tok,
+                                   at<int32_t>(ws, w, R_PERM_SLOT), inv, gw, with_shared,
+                                   max_tiles, tiles, s));
+    tiles_built = true;
+  } else if (!permuted && !perm_in_gate_up) {
     LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
                              at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
                              at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
+  }
   LBMOE_TRY(ev->mark(s));
   void* act = at<void>(ws, w, R_ACT);
   void* out = at<void>(ws, w, R_OUT);
@@ -212,9 +229,8 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     const int64_t rows = T * k + (with_shared ? T : 0);
     LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
     if (use_tiled(gw, T, k) && tiled_fp8_supported(gw, T, rows)) {
-      int32_t* tiles = at<int32_t>(ws, w, R_TILES);
-      const int max_tiles = tiled_max_tiles(rows, gw.groups);
-      LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
+      if (!tiles_built)
+        LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
       LBMOE_TRY(launch_gate_up_tiled_fp8(gw, xq, xs, perm_tok, tiles, max_tiles, Imax, actq, acts,
                                          s));
       LBMOE_TRY(ev->mark(s));
@@ -233,9 +249,8 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
   if (rt && use_tiled(gw, T, k)) return LBMOE_ERR_SHAPE;   // not reached (see forward_impl)
   if (use_tiled(gw, T, k)) {
     // prefill-sized batch: LDS-tiled MFMA GEMMs over a device-built token-tile list
-    int32_t* tiles = at<int32_t>(ws, w, R_TILES);
-    const int max_tiles = tiled_max_tiles(T * k + (with_shared ? T : 0), gw.groups);
-    LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
+    if (!tiles_built)
+      LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
     LBMOE_TRY(launch_gate_up_tiled(gw, x, perm_tok, tiles, max_tiles, T, Imax, act, s));
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(launch_down_tiled(gw, act, Imax, tiles, max_tiles, T, out, s));
@@ -334,6 +349,16 @@ struct NormArgs {
   void* residual_out;
 };
 
+// Whether the block routes through launch_router_route: the tiled router over at most 128
+// experts, with the tiled expert GEMMs after it (their tile list is built with the scatter).
+static bool route_in_router(const lbmoe_layer& L, int64_t T, bool sh) {
+  const int E = L.num_experts, H = L.hidden_size, k = L.top_k;
+  if (!router_is_tiled(T, E, H) || !router_route_supported(E, H, k)) return false;
+  const GroupWeights gw = group_weights(L, sh, T);
+  if (!use_tiled(gw, T, k)) return false;
+  return !is_fp8(L) || tiled_fp8_supported(gw, T, T * k + (sh ? T : 0));
+}
+
 static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, void* y,
                             void* workspace, size_t workspace_bytes, void* stream,
                             StageEvents* ev, const NormArgs* norm = nullptr) {
@@ -354,6 +379,18 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
   void* topw = at<void>(ws, w, R_TOPW);
   float* sgate = sh ? at<float>(ws, w, R_SGATE) : nullptr;
   LBMOE_TRY(ev->mark(s));
+  if (!norm && route_in_router(L, T, sh)) {
+    // logits, selection and the permutation's count pass in one launch (profiled calls time it
+    // as the router stage, the routing stage then being empty)
+    LBMOE_TRY(launch_router_route(x, L.gate_weight, L.logit_bias, L.shared_expert_gate, T,
+                                  L.num_experts, L.hidden_size, L.top_k, logits,
+                                  static_cast<int32_t*>(idx), topw, sgate,
+                                  at<int32_t>(ws, w, R_HIST), at<int32_t>(ws, w, R_LRANK), s));
+    LBMOE_TRY(ev->mark(s));
+    LBMOE_TRY(ev->mark(s));
+    return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, false, nullptr, true,
+                       true);
+  }
   if (norm) {
     // x is the attention output: the block's input is the normalised residual sum
     void* xn = at<void>(ws, w, R_XN);

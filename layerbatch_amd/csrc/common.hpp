@@ -108,6 +108,17 @@ __device__ __forceinline__ int mask_rank(uint64_t m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
 }
 
+// Stable in-wave match: the lanes of m whose value e (below 2^nbits) equals this lane's, one
+// ballot per bit. With mask_rank, lanes of equal value get consecutive ranks in lane order.
+__device__ __forceinline__ uint64_t match_expert(int e, uint64_t m, int nbits) {
+  for (int b = 0; b < nbits; ++b) {
+    const bool on = (e >> b) & 1;
+    const uint64_t bal = __ballot(on);
+    m &= on ? bal : ~bal;
+  }
+  return m;
+}
+
 __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

@@ -230,6 +230,24 @@ hipError_t launch_down_tiled_fp8(const GroupWeights& gw, const void* actq, const
                                  int act_ld, const int32_t* tiles, int max_tiles, void* out,
                                  hipStream_t s);
 bool tiled_router_supported(int E, int H);
+// whether launch_router_logits runs the LDS-tiled router for this batch
+bool router_is_tiled(int64_t T, int E, int H);
+// Router logits + selection + the permutation's count pass in one launch (E <= 128), then the
+// per-expert scan (launch_perm_scan over router_route_chunks(T, k) chunks) and the scatter with
+// the tile list (launch_scatter_build).
+bool router_route_supported(int E, int H, int k);
+int64_t router_route_chunks(int64_t T, int k);
+hipError_t launch_router_route(const void* x, const void* wg, const float* bias, const void* w_sg,
+                               int64_t T, int E, int H, int k, void* logits, int32_t* idx,
+                               void* topw, float* sgate, int32_t* hist, int32_t* lrank,
+                               hipStream_t s);
+hipError_t launch_perm_scan(const int32_t* hist, int nchunks, int E, int32_t* base,
+                            int32_t* totals, hipStream_t s);
+hipError_t launch_scatter_build(const int32_t* idx, int64_t T, int k, const int32_t* base,
+                                const int32_t* counts, const int32_t* lrank, int32_t* offsets,
+                                int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,
+                                const GroupWeights& gw, bool shared, int max_tiles,
+                                int32_t* tiles, hipStream_t s);
 hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, int E, int H,
                                       void* logits, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t s);

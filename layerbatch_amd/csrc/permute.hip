@@ -28,16 +28,6 @@ __device__ __forceinline__ int load_expert(const void* idx, int64_t i) {
   else return reinterpret_cast<const int32_t*>(idx)[i];
 }
 
-// Stable in-wave match: lanes with equal expert id (among `m`) get consecutive ranks.
-__device__ __forceinline__ uint64_t match_expert(int e, uint64_t m, int nbits) {
-  for (int b = 0; b < nbits; ++b) {
-    const bool on = (e >> b) & 1;
-    const uint64_t bal = __ballot(on);
-    m &= on ? bal : ~bal;
-  }
-  return m;
-}
-
 // Ranks one chunk's entries. Returns per-lane (expert, rank) for round r in e_out/rk_out.
 // All expert ids of the chunk are loaded before the ranking so the loads overlap.
 template <int IB, int ROUNDS>
@@ -341,6 +331,12 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
   perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
   perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, counts,
                                        offsets, lrank, perm_tok, perm_slot, inv);
+  return hipGetLastError();
+}
+
+hipError_t launch_perm_scan(const int32_t* hist, int nchunks, int E, int32_t* base,
+                            int32_t* totals, hipStream_t s) {
+  perm_expert_scan<<<E, 64, 0, s>>>(hist, nchunks, base, totals);
   return hipGetLastError();
 }
 

@@ -1,7 +1,8 @@
 // One token's router selection, executed by one wave: softmax -> top-k -> renormalise -> bf16
 // and the shared-expert gate (the algorithm and its reference lines are described in
-// route.hip). Shared by the route kernel and the fused route + permutation kernel of small
-// batches.
+// route.hip). Shared by the route kernel, the fused route + permutation kernel of small
+// batches, the decode gate_up kernel that routes inline, and the tiled router that selects
+// from its own logits.
 #pragma once
 
 #include <float.h>
@@ -36,55 +37,21 @@ __device__ __forceinline__ int wave_min_i32(int v) {
   return min(min(r0, r1), min(r2, r3));
 }
 
-// Token t's selection: idx_out[t*k + s] (idx_bytes 4 or 8), topw[t*k + s] and sgate[t] (each
-// when not null). Every lane of the wave must call it; it uses no LDS and no barrier.
+// Selection from one token's scores, z[j] = logit + bias of expert j * 64 + lane (-inf past E
+// and for NaN), every lane of the wave calling it: writes idx_out[o + s] (idx_bytes 4 or 8),
+// topw[o + s] (when not null) and idx_lds[s] (a second copy of the ids, when not null), o = t*k.
 template <int EPL>
-__device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
-                                            const float* __restrict__ bias,
-                                            const uint16_t* __restrict__ x,
-                                            const uint16_t* __restrict__ w_sg, int t, int E,
-                                            int H, int k, void* idx_out, int idx_bytes,
-                                            uint16_t* __restrict__ topw,
-                                            float* __restrict__ sgate) {
+__device__ __forceinline__ void route_select(const float (&z)[EPL], int E, int k, int64_t o,
+                                             void* idx_out, int idx_bytes,
+                                             uint16_t* __restrict__ topw, int32_t* idx_lds) {
   const int lane = lane_id();
-  const uint16_t* lrow = logits + static_cast<int64_t>(t) * E;
-  float z[EPL];
   uint32_t key[EPL];
   float m = -INFINITY;
-  // unconditional loads (lanes past E read expert E-1 and are masked): a load under a
-  // condition would make the compiler wait for it before the next one is issued
-  uint16_t lv[EPL];
-  float bv[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = min(j * kWave + lane, E - 1);
-    lv[j] = lrow[e];
-    bv[j] = bias ? bias[e] : 0.f;
-  }
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
-    float v = bf2f(lv[j]) + bv[j];
-    if (!(v == v) || e >= E) v = -INFINITY;   // a NaN logit is never preferred
-    z[j] = v;
-    key[j] = e < E ? order_key(v) : 0u;       // 0 is below every valid key
-    m = fmaxf(m, v);
-  }
-  // the shared-expert gate, its loads in flight together with the logits'
-  if (sgate != nullptr) {
-    const uint16_t* xr = x + static_cast<int64_t>(t) * H;
-    float d = 0.f;
-    for (int c = lane * 8; c < H; c += kWave * 8) {
-      const u32x4 a = ld16(xr + c);
-      const u32x4 b = ld16(w_sg + c);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        d += bf_lo(a[q]) * bf_lo(b[q]);
-        d += bf_hi(a[q]) * bf_hi(b[q]);
-      }
-    }
-    d = round_bf(wave_sum(d));
-    if (lane == 0) sgate[t] = 1.0f / (1.0f + expf(-d));
+    key[j] = e < E ? order_key(z[j]) : 0u;             // 0 is below every valid key
+    m = fmaxf(m, z[j]);
   }
   m = wave_max(m);
   float part = 0.f;
@@ -130,11 +97,159 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
   }
   const float psum = wave_sum(p);
   if (lane < k) {
-    const int64_t o = static_cast<int64_t>(t) * k + lane;
-    if (topw != nullptr) topw[o] = static_cast<uint16_t>(f2bf(p / psum));
-    if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o] = my_e;
-    else reinterpret_cast<int32_t*>(idx_out)[o] = my_e;
+    if (topw != nullptr) topw[o + lane] = static_cast<uint16_t>(f2bf(p / psum));
+    if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o + lane] = my_e;
+    else reinterpret_cast<int32_t*>(idx_out)[o + lane] = my_e;
+    if (idx_lds != nullptr) idx_lds[lane] = my_e;
   }
+}
+
+// Reductions over the 8-lane groups of a wave (lanes 8g .. 8g+7): two quad swaps, then the
+// mirror within each half row, after which every lane of the group holds the result.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float group8_max(float v) {
+  v = fmaxf(v, dpp_f32<0xb1>(v));
+  v = fmaxf(v, dpp_f32<0x4e>(v));
+  return fmaxf(v, dpp_f32<0x141>(v));
+}
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  return v + dpp_f32<0x141>(v);
+}
+__device__ __forceinline__ uint32_t group8_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(dpp_i32<0xb1>(static_cast<int>(v))));
+  v = max(v, static_cast<uint32_t>(dpp_i32<0x4e>(static_cast<int>(v))));
+  return max(v, static_cast<uint32_t>(dpp_i32<0x141>(static_cast<int>(v))));
+}
+__device__ __forceinline__ int group8_min_i32(int v) {
+  v = min(v, dpp_i32<0xb1>(v));
+  v = min(v, dpp_i32<0x4e>(v));
+  return min(v, dpp_i32<0x141>(v));
+}
+
+// route_select for 8 tokens at once, one per 8-lane group: lane u of a group holds the scores
+// of experts u, u + 8, ..., z[j] of expert 8j + u (-inf past E and for NaN), and the group's
+// reductions stay within it, so a wave selects 8 tokens in the time route_select takes for
+// one. The same order (descending score, ties to the lower expert); the softmax sums run in
+// another order, so a weight may differ from route_select's by one bf16 step. Lane u writes
+// slots u and u + 8 (k <= 16): idx_out[o + s], topw[o + s] (when not null) and idx_lds[s]
+// (when not null); lanes with write == false only take part in the reductions.
+template <int EPG>
+__device__ __forceinline__ void route_select8(const float (&z)[EPG], int E, int k, int64_t o,
+                                              bool write, int32_t* __restrict__ idx_out,
+                                              uint16_t* __restrict__ topw, int32_t* idx_lds) {
+  const int u = lane_id() & 7;
+  uint32_t key[EPG];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < EPG; ++j) {
+    key[j] = 8 * j + u < E ? order_key(z[j]) : 0u;           // 0 is below every valid key
+    m = fmaxf(m, z[j]);
+  }
+  m = group8_max(m);
+  float part = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPG; ++j)
+    if (8 * j + u < E) part += expf(z[j] - m);
+  const float S = group8_sum(part);
+  int my_e[2] = {0, 0};
+  uint32_t my_key[2] = {0u, 0u};
+  for (int r = 0; r < k; ++r) {
+    uint32_t best = key[0];
+    int bj = 0;
+#pragma unroll
+    for (int j = 1; j < EPG; ++j)
+      if (key[j] > best) {
+        best = key[j];
+        bj = j;
+      }
+    const uint32_t gmax = group8_max_u32(best);
+    const int win = group8_min_i32(best == gmax ? 8 * bj + u : 0x7fffffff);
+#pragma unroll
+    for (int j = 0; j < EPG; ++j)
+      if (8 * j + u == win) key[j] = 0u;
+    if ((r & 7) == u) {
+      my_e[r >> 3] = win;
+      my_key[r >> 3] = gmax;
+    }
+  }
+  float p[2], ps = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t kk = my_key[h];
+    const uint32_t bits = (kk & 0x80000000u) ? (kk & 0x7fffffffu) : ~kk;   // key -> z
+    p[h] = u + 8 * h < k ? expf(__uint_as_float(bits) - m) / S : 0.f;
+    ps += p[h];
+  }
+  const float psum = group8_sum(ps);
+  if (!write) return;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = u + 8 * h;
+    if (r < k) {
+      if (topw != nullptr) topw[o + r] = static_cast<uint16_t>(f2bf(p[h] / psum));
+      idx_out[o + r] = my_e[h];
+      if (idx_lds != nullptr) idx_lds[r] = my_e[h];
+    }
+  }
+}
+
+// sgate[t] = sigmoid(bf16(x[t] . w_sg)), every lane of the wave calling it.
+__device__ __forceinline__ void shared_gate(const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ w_sg, int t, int H,
+                                            float* __restrict__ sgate) {
+  const int lane = lane_id();
+  const uint16_t* xr = x + static_cast<int64_t>(t) * H;
+  float d = 0.f;
+  for (int c = lane * 8; c < H; c += kWave * 8) {
+    const u32x4 a = ld16(xr + c);
+    const u32x4 b = ld16(w_sg + c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      d += bf_lo(a[q]) * bf_lo(b[q]);
+      d += bf_hi(a[q]) * bf_hi(b[q]);
+    }
+  }
+  d = round_bf(wave_sum(d));
+  if (lane == 0) sgate[t] = 1.0f / (1.0f + expf(-d));
+}
+
+// Token t's selection: idx_out[t*k + s] (idx_bytes 4 or 8), topw[t*k + s] and sgate[t] (each
+// when not null). Every lane of the wave must call it; it uses no LDS and no barrier.
+template <int EPL>
+__device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
+                                            const float* __restrict__ bias,
+                                            const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ w_sg, int t, int E,
+                                            int H, int k, void* idx_out, int idx_bytes,
+                                            uint16_t* __restrict__ topw,
+                                            float* __restrict__ sgate) {
+  const int lane = lane_id();
+  const uint16_t* lrow = logits + static_cast<int64_t>(t) * E;
+  // unconditional loads (lanes past E read expert E-1 and are masked): a load under a
+  // condition would make the compiler wait for it before the next one is issued
+  uint16_t lv[EPL];
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = min(j * kWave + lane, E - 1);
+    lv[j] = lrow[e];
+    bv[j] = bias ? bias[e] : 0.f;
+  }
+  float z[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = j * kWave + lane;
+    const float v = bf2f(lv[j]) + bv[j];
+    z[j] = (!(v == v) || e >= E) ? -INFINITY : v;      // a NaN logit is never preferred
+  }
+  // the shared-expert gate, its loads in flight together with the logits'
+  if (sgate != nullptr) shared_gate(x, w_sg, t, H, sgate);
+  route_select<EPL>(z, E, k, static_cast<int64_t>(t) * k, idx_out, idx_bytes, topw, nullptr);
 }
 
 }  // namespace lbmoe

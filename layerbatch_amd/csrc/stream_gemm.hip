@@ -299,9 +299,13 @@ static hipError_t launch_router_decode(const uint16_t* x, const NormIn& nm, cons
 // Token count from which the router logits run as an LDS-tiled MFMA GEMM.
 constexpr int64_t kTiledRouterMinTokens = 1024;
 
+bool router_is_tiled(int64_t T, int E, int H) {
+  return T >= kTiledRouterMinTokens && tiled_router_supported(E, H);
+}
+
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,
                                 void* logits, hipStream_t s) {
-  if (T >= kTiledRouterMinTokens && tiled_router_supported(E, H))
+  if (router_is_tiled(T, E, H))
     return launch_router_logits_tiled(x, wg, T, E, H, logits, s);
   return launch_router_decode<false>(static_cast<const uint16_t*>(x), NormIn{}, wg, T, E, H,
                                      logits, s);

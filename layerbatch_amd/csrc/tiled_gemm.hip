@@ -35,6 +35,7 @@
 // then the up rows of the same channels, so SiLU*mul pairs accumulators in registers.
 #include "common.hpp"
 #include "internal.hpp"
+#include "route_token.hpp"
 #include "tiled_shape.hpp"
 
 namespace lbmoe {
@@ -144,10 +145,10 @@ __host__ __device__ inline int32_t* queue_base(int32_t* tiles, int max_tiles, in
 // group's first row in the sorted rows, group's row count}. list: the tile list (2 ints per
 // entry); grp: per group (first row, row count).
 __device__ __forceinline__ void write_dispatch(const int* list, const int2* grp, int n_all,
-                                              int n_wide, int n_wtiles, int wt_cols, int grid,
-                                              int E, int I, int Is, u32x4* table) {
+                                              int n_wide, int n_wtiles, int wt_cols, int b_lo,
+                                              int b_hi, int E, int I, int Is, u32x4* table) {
   const int W = n_wide * n_wtiles, N = (n_all - n_wide) * n_wtiles;
-  for (int b = threadIdx.x; b < grid; b += blockDim.x) {
+  for (int b = b_lo + static_cast<int>(threadIdx.x); b < b_hi; b += blockDim.x) {
     const int item = dispatch_item(b, W, N);
     u32x4 ent = {0xffffffffu, 0u, 0u, 0u};
     if (item >= 0) {
@@ -165,27 +166,43 @@ __device__ __forceinline__ void write_dispatch(const int* list, const int2* grp,
 }
 
 // Tile lists up to this many entries are also assembled in LDS, where the dispatch tables
-// read them back; longer ones are read back from memory.
+// read them back; longer ones are read back from memory. With the list in LDS, up to
+// kBuildBlocks workgroups write the dispatch tables: each assembles the (short) list itself and
+// writes its share of the entries, so the table loop (two 64-bit divisions per entry) does not
+// hold one CU for the whole launch. Workgroup 0 alone writes the list, its counts and the queues.
 constexpr int kLdsListEntries = 4096;
+constexpr int kBuildBlocks = 32;
+constexpr int kBuildEntriesPerBlock = 256;
 
-__global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
-                                                           const int32_t* __restrict__ offsets,
-                                                           int E, int shared, int T, int sh_row0,
-                                                           int max_tiles, int wide, int narrow,
-                                                           int tiny, int I, int Is, int H, int grid_gu,
-                                                           int grid_dn, int32_t* __restrict__ tiles) {
+// The tile list and dispatch tables, by workgroup bidx of nblocks (1024 threads each; see
+// kBuildBlocks). offsets == nullptr: the groups' first rows are the exclusive scan of counts
+// (E <= 1024), computed here.
+__device__ __forceinline__ void build_tiles_body(const int32_t* __restrict__ counts,
+                                                 const int32_t* __restrict__ offsets, int E,
+                                                 int shared, int T, int sh_row0, int max_tiles,
+                                                 int wide, int narrow, int tiny, int I, int Is,
+                                                 int H, int grid_gu, int grid_dn,
+                                                 int32_t* __restrict__ tiles, int bidx,
+                                                 int nblocks) {
   __shared__ int wsum[16];
   __shared__ int s_list[2 * kLdsListEntries];
   __shared__ int2 s_grp[1025];
+  __shared__ int s_first[1024];
   const int G = E + shared;
   const int tid = threadIdx.x;
   const bool in_lds = max_tiles <= kLdsListEntries;
+  if (offsets == nullptr) {
+    int ex;
+    block_scan_1024(tid < E ? counts[tid] : 0, ex, wsum);
+    if (tid < E) s_first[tid] = ex;
+    __syncthreads();
+  }
   const int per = (G + 1023) / 1024;
   const int lo = min(G, tid * per), hi = min(G, lo + per);
   int lw = 0, ln = 0, nw, nn, nt;
   for (int g = lo; g < hi; ++g) {
     const int n = g < E ? counts[g] : T;
-    s_grp[g] = int2{g < E ? offsets[g] : sh_row0, n};
+    s_grp[g] = int2{g < E ? (offsets ? offsets[g] : s_first[g]) : sh_row0, n};
     group_tiles(n, wide, narrow, tiny, nw, nn, nt);
     lw += nw;
     ln += nn + nt;
@@ -194,10 +211,13 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   const int tw = block_scan_1024(lw, pw, wsum);
   const int tn = block_scan_1024(ln, pn, wsum);
   pn += tw;
+  const bool lead = bidx == 0;
   auto put = [&](int pos, int g, int e) {
     if (pos >= max_tiles) return;
-    tiles[2 * pos] = g;
-    tiles[2 * pos + 1] = e;
+    if (lead) {
+      tiles[2 * pos] = g;
+      tiles[2 * pos + 1] = e;
+    }
     if (in_lds) {
       s_list[2 * pos] = g;
       s_list[2 * pos + 1] = e;
@@ -210,12 +230,12 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
     if (nt) put(pn++, g, (nw * wide) | kTinyFlag);
   }
   const int n_all = min(tw + tn, max_tiles), n_wide = min(tw, max_tiles);
-  if (tid == 0) {
+  if (lead && tid == 0) {
     tiles[2 * max_tiles] = n_all;
     tiles[2 * max_tiles + 1] = n_wide;
   }
   if (grid_gu + grid_dn == 0) return;
-  if (tid < 8) {
+  if (lead && tid < 8) {
     // gate_up work queue of XCD x: its slots of the dispatch table (slot j = entry j * 8 + x)
     // that dispatch_item fills, and a counter from zero
     const int x = tid, n_wt = I > Is ? I / (kWM / 2) : Is / (kWM / 2);
@@ -230,9 +250,66 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
   __syncthreads();                           // the list is complete (and visible to the block)
   const int* list = in_lds ? s_list : tiles;
   u32x4* tab = reinterpret_cast<u32x4*>(tiles + table_base(max_tiles));
+  // this workgroup's share of the entries, gate_up's table then down's
+  const int total = grid_gu + grid_dn, share = (total + nblocks - 1) / nblocks;
+  const int b_lo = min(total, bidx * share), b_hi = min(total, b_lo + share);
   write_dispatch(list, s_grp, n_all, n_wide, I > Is ? I / (kWM / 2) : Is / (kWM / 2), kWM / 2,
-                 grid_gu, E, I, Is, tab);
-  write_dispatch(list, s_grp, n_all, n_wide, H / kWM, 0, grid_dn, E, I, Is, tab + grid_gu);
+                 min(b_lo, grid_gu), min(b_hi, grid_gu), E, I, Is, tab);
+  write_dispatch(list, s_grp, n_all, n_wide, H / kWM, 0, max(b_lo - grid_gu, 0),
+                 max(b_hi - grid_gu, 0), E, I, Is, tab + grid_gu);
+}
+
+__global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __restrict__ counts,
+                                                           const int32_t* __restrict__ offsets,
+                                                           int E, int shared, int T, int sh_row0,
+                                                           int max_tiles, int wide, int narrow,
+                                                           int tiny, int I, int Is, int H, int grid_gu,
+                                                           int grid_dn, int32_t* __restrict__ tiles) {
+  build_tiles_body(counts, offsets, E, shared, T, sh_row0, max_tiles, wide, narrow, tiny, I, Is,
+                   H, grid_gu, grid_dn, tiles, blockIdx.x, gridDim.x);
+}
+
+// Last pass of the permutation of router_route_kernel's selection, with the tile list built in
+// the same launch. Routing entries come in chunks c = s * nb + b (slot s, 64-token block b),
+// which in this order follow the reference's (slot, token) order; hist/base hold per expert and
+// chunk the count and the exclusive prefix (base, from perm_expert_scan) and lrank each entry's
+// rank among its chunk's entries of the same expert. Workgroups below n_scatter place 16 chunks
+// each (a wave per chunk, a lane per token), pos = first row of the expert + base + rank; the
+// others build the tile list and dispatch tables from the expert totals.
+__global__ __launch_bounds__(1024) void scatter_build_kernel(
+    const int32_t* __restrict__ idx, int T, int k, int nb, const int32_t* __restrict__ base,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ lrank,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tok, int32_t* __restrict__ perm_slot,
+    int32_t* __restrict__ inv, int n_scatter, int E, int shared, int sh_row0, int max_tiles,
+    int wide, int narrow, int tiny, int I, int Is, int H, int grid_gu, int grid_dn,
+    int32_t* __restrict__ tiles) {
+  if (static_cast<int>(blockIdx.x) >= n_scatter) {
+    build_tiles_body(counts, nullptr, E, shared, T, sh_row0, max_tiles, wide, narrow, tiny, I, Is,
+                     H, grid_gu, grid_dn, tiles, blockIdx.x - n_scatter, gridDim.x - n_scatter);
+    return;
+  }
+  __shared__ int wsum[16];
+  __shared__ int s_off[1024];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  int ex;
+  const int total = block_scan_1024(tid < E ? counts[tid] : 0, ex, wsum);
+  if (tid < E) s_off[tid] = ex;
+  if (blockIdx.x == 0) {
+    if (tid < E) offsets[tid] = ex;
+    if (tid == 0) offsets[E] = total;
+  }
+  __syncthreads();
+  const int nchunks = k * nb, c = blockIdx.x * 16 + wave;
+  if (c >= nchunks) return;
+  const int s = c / nb, t = (c - s * nb) * 64 + lane;
+  if (t >= T) return;
+  const int64_t ts = static_cast<int64_t>(t) * k + s;
+  const int e = idx[ts];                     // the router's own selection: always in [0, E)
+  const int pos = s_off[e] + base[static_cast<int64_t>(e) * nchunks + c] +
+                  lrank[static_cast<int64_t>(s) * T + t];
+  perm_tok[pos] = t;
+  perm_slot[pos] = s;
+  inv[ts] = pos;
 }
 
 // ---- one token tile --------------------------------------------------------------------------
@@ -240,9 +317,6 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(const int32_t* __rest
 // kRouter: logits[t, e] = x[t] . Wg[e] (gw.gate_up holds the router weight, gw.E its rows).
 enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 
-// Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
-// expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
-// src (down) / dst.
 // Work queue of a persistent workgroup. XCD x's queue holds the dispatch-table entries
 // table[j * 8 + x], j < its length (the items a launch of one workgroup per entry would run on
 // that XCD, in the same order); its counter hands them out. A workgroup takes entries from its
@@ -278,11 +352,19 @@ __device__ __forceinline__ u32x4 queue_fetch(WorkQueue& wq) {
   return u32x4{0xffffffffu, 0u, 0u, 0u};
 }
 
+// Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
+// expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
+// src (down) / dst.
 // PERSIST: called from the persistent kernel, which passes its work queue. The tile then claims
 // the next entry of the home queue after k-tile nk - 2's barrier, loads it at the start of the
 // epilogue, and leaves it (or, when the claim found nothing, a synchronously fetched entry) in
 // the ring's last 16 bytes, which no staged tile reaches.
-template <int MODE, class S, int kLdsCap = kLdsU4, bool PERSIST = false>
+// STAGE (router only): the tile's logits are also left in LDS, rounded to bf16, as rows of
+// kStagedLogitStride entries per token (staged_logits), for a selection that follows in the
+// same workgroup.
+template <class S>
+constexpr int kStagedLogitStride = S::kRows + 8;   // uint16 entries; + 8 against bank conflicts
+template <int MODE, class S, int kLdsCap = kLdsU4, bool PERSIST = false, bool STAGE = false>
 __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint16_t* __restrict__ src,
                                              int src_ld, const int32_t* __restrict__ perm_tok,
                                              int g, int r0, int n, int row0, int wt,
@@ -578,6 +660,40 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     }
     ring_barrier();
     store_staged<kCols, S::kWT>(lds, dst, dst_ld, row0, r0, n, c0);
+  } else if constexpr (STAGE) {
+    // logits through LDS: staged rows, then whole rows stored with 16-byte lanes
+    constexpr int kStride = kStagedLogitStride<S>;
+    static_assert(S::kWT * kStride * 2 <= kLdsCap * 16, "staged logits exceed the ring");
+    ring_barrier();                                           // every wave is done with the ring
+    uint16_t* sl = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int tl = wn * (kNT * 32) + 32 * t + col;          // token within the tile
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int e = wm * kRW + 32 * i + 8 * v4 + rq;     // expert within the tile
+          *reinterpret_cast<u32x2*>(sl + tl * kStride + e) =
+              u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
+                    pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
+        }
+    }
+    ring_barrier();
+    const int E = gw.E, ntok = min(S::kWT, n - r0), ne = min(kRows, E - c0);
+    if ((ne & 7) == 0 && (dst_ld & 7) == 0 && (c0 & 7) == 0) {
+      const int cpr = ne / 8;                                 // 16-byte chunks per row
+      for (int i = threadIdx.x; i < ntok * cpr; i += kThreads) {
+        const int tl = i / cpr, c = i - tl * cpr;
+        *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + 8 * c) =
+            *reinterpret_cast<const u32x4*>(sl + tl * kStride + 8 * c);
+      }
+    } else {
+      for (int i = threadIdx.x; i < ntok * ne; i += kThreads) {
+        const int tl = i / ne, e = i - tl * ne;
+        dst[static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + e] = sl[tl * kStride + e];
+      }
+    }
   } else {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
@@ -618,6 +734,92 @@ void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
   tile_product<kRouter, S, S::kRingU4>(gw, x, gw.H, nullptr, 0, ti * S::kWT, T, 0,
                                                      wt, logits, gw.E, lds);
 }
+
+// Router logits, selection and the first permutation pass in one workgroup per 64-token block
+// b (E <= 128, so one tile holds every expert): the tile's logits stay in LDS (STAGE), and each
+// wave selects 8 tokens at once from them (route_select8, an 8-lane group per token, experts
+// 8j + u on lane u of the group) and keeps their ids in LDS; then, for each slot s, a wave ranks
+// the block's 64 entries of chunk c = s * nb + b among equal experts (ballot match, in token
+// order) into lrank and writes the chunk's per-expert counts to hist[e * k * nb + c].
+// perm_expert_scan and scatter_build_kernel finish the sort. Saves the route and count
+// launches and the logits' round trip. EPG: experts per lane, ceil(E / 8) rounded up to 8 or 16.
+constexpr int kRouteMaxK = 16;
+template <int EPG>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
+void router_route_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
+                         const float* __restrict__ bias, const uint16_t* __restrict__ w_sg, int k,
+                         int nbits, int nb, uint16_t* __restrict__ logits, int32_t* __restrict__ idx,
+                         uint16_t* __restrict__ topw, float* __restrict__ sgate,
+                         int32_t* __restrict__ hist, int32_t* __restrict__ lrank) {
+  using S = RouterShape128;
+  constexpr int kStride = kStagedLogitStride<S>, kPerWave = S::kWT / kWaves;
+  static_assert(kPerWave == kWave / 8, "a wave selects one token per 8-lane group");
+  static_assert(8 * EPG <= S::kRows, "experts per lane exceed the tile");
+  // The ring is the kernel's only LDS object: the ids and counts live in it, behind the staged
+  // logits. With a second __shared__ array in the kernel the compiler made every LDS read of
+  // the k-loop wait for all global->LDS copies in flight (s_waitcnt vmcnt(0)), which drained
+  // the ring each k-tile (the tile took 30 instead of 19 us at Qwen3-30B-A3B T=8192).
+  __shared__ u32x4 lds[S::kRingU4];
+  constexpr int kStagedBytes = S::kWT * kStride * 2;
+  static_assert(kStagedBytes % 16 == 0 &&
+                    kStagedBytes + (S::kWT * kRouteMaxK + kWaves * S::kRows) * 4 <= S::kRingU4 * 16,
+                "ids and counts exceed the ring");
+  int32_t* s_idx = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(lds) + kStagedBytes);
+  int32_t* s_cnt = s_idx + S::kWT * kRouteMaxK;              // [kWaves][S::kRows]
+  const int b = xcd_item(blockIdx.x, nb);
+  if (b < 0) return;
+  const int E = gw.E, H = gw.H, t0 = b * S::kWT, nt = min(S::kWT, T - t0);
+  tile_product<kRouter, S, S::kRingU4, false, true>(gw, x, H, nullptr, 0, t0, T, 0, 0, logits, E,
+                                                    lds);
+  const uint16_t* sl = reinterpret_cast<const uint16_t*>(lds);
+  const int lane = lane_id(), u = lane & 7;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (sgate != nullptr) {
+    // the shared-expert gate of the wave's tokens, a whole wave per token
+    for (int i = 0; i < kPerWave; ++i) {
+      const int tl = w * kPerWave + i;                        // the same for the whole wave
+      if (tl >= nt) break;
+      shared_gate(x, w_sg, t0 + tl, H, sgate);
+    }
+  }
+  const int tl = w * kPerWave + (lane >> 3);                  // this lane group's token
+  const bool ok = tl < nt;
+  const int tr = ok ? tl : 0;                                 // past the batch: token 0's row
+  float z[EPG];
+#pragma unroll
+  for (int j = 0; j < EPG; ++j) {
+    const int e = 8 * j + u, ec = min(e, E - 1);
+    const float v = bf2f(sl[tr * kStride + ec]) + (bias ? bias[ec] : 0.f);
+    z[j] = (!(v == v) || e >= E) ? -INFINITY : v;             // a NaN logit is never preferred
+  }
+  route_select8<EPG>(z, E, k, static_cast<int64_t>(t0 + tl) * k, ok, idx, topw, s_idx + tr * k);
+  __syncthreads();
+  const int nchunks = k * nb;
+  for (int s = w; s < k; s += kWaves) {
+    const int c = s * nb + b;
+    int32_t* cnt = s_cnt + w * S::kRows;
+    for (int e = lane; e < E; e += kWave) cnt[e] = 0;
+    const bool valid = lane < nt;
+    const int e = valid ? s_idx[lane * k + s] : 0;            // in [0, E): the selection's own
+    const uint64_t m = match_expert(e, __ballot(valid), nbits);
+    const int rank = mask_rank(m);
+    if (valid) {
+      lrank[static_cast<int64_t>(s) * T + t0 + lane] = rank;
+      if (rank == 0) cnt[e] = __popcll(m);                  // a wave's LDS accesses are in order
+    }
+    for (int e2 = lane; e2 < E; e2 += kWave)
+      hist[static_cast<int64_t>(e2) * nchunks + c] = cnt[e2];
+  }
+}
+
+// explicit instantiations: with only the two launches in launch_router_route, the host pass left
+// the second one's launch stub undefined in the library
+template __global__ void router_route_kernel<8>(GroupWeights, const uint16_t*, int, const float*,
+                                                const uint16_t*, int, int, int, uint16_t*,
+                                                int32_t*, uint16_t*, float*, int32_t*, int32_t*);
+template __global__ void router_route_kernel<16>(GroupWeights, const uint16_t*, int, const float*,
+                                                const uint16_t*, int, int, int, uint16_t*,
+                                                int32_t*, uint16_t*, float*, int32_t*, int32_t*);
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -714,14 +916,21 @@ const u32x4* tiled_table(const GroupWeights& gw, const int32_t* tiles, int max_t
   return gate_up ? t : t + tiled_grid(gw, max_tiles, true);
 }
 
+// Workgroups that build a tile list with `entries` dispatch-table entries.
+static int build_blocks(int max_tiles, int entries) {
+  if (max_tiles > kLdsListEntries) return 1;   // a list past kLdsListEntries is read back from memory
+  const int blocks = (entries + kBuildEntriesPerBlock - 1) / kBuildEntriesPerBlock;
+  return blocks < 1 ? 1 : (blocks > kBuildBlocks ? kBuildBlocks : blocks);
+}
+
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
                               bool shared, int64_t T, int max_tiles, int32_t* tiles,
                               hipStream_t s) {
-  build_tiles_kernel<<<1, 1024, 0, s>>>(counts, offsets, gw.E, shared ? 1 : 0,
-                                        static_cast<int>(T), gw.sh_row0, max_tiles, Wide::kWT,
-                                        Narrow::kWT, Tiny::kWT, gw.I, gw.Is, gw.H,
-                                        tiled_grid(gw, max_tiles, true),
-                                        tiled_grid(gw, max_tiles, false), tiles);
+  const int grid_gu = tiled_grid(gw, max_tiles, true), grid_dn = tiled_grid(gw, max_tiles, false);
+  build_tiles_kernel<<<build_blocks(max_tiles, grid_gu + grid_dn), 1024, 0, s>>>(counts, offsets, gw.E, shared ? 1 : 0,
+                                             static_cast<int>(T), gw.sh_row0, max_tiles,
+                                             Wide::kWT, Narrow::kWT, Tiny::kWT, gw.I, gw.Is, gw.H,
+                                             grid_gu, grid_dn, tiles);
   return hipGetLastError();
 }
 
@@ -784,6 +993,61 @@ static hipError_t launch_router_shape(const GroupWeights& gw, const void* x, int
   router_tiled_kernel<S><<<round8(n_ttiles * n_wtiles), kThreads, 0, s>>>(
       gw, static_cast<const uint16_t*>(x), static_cast<int>(T), n_wtiles,
       static_cast<uint16_t*>(logits));
+  return hipGetLastError();
+}
+
+bool router_route_supported(int E, int H, int k) {
+  return E <= RouterShape128::kRows && tiled_router_supported(E, H) && k >= 1 && k <= kRouteMaxK &&
+         k <= E;
+}
+
+int64_t router_route_chunks(int64_t T, int k) {
+  return (T + RouterShape128::kWT - 1) / RouterShape128::kWT * k;
+}
+
+static int bits_of(int E) {
+  int n = 0;
+  while ((1 << n) < E) ++n;
+  return n;
+}
+
+hipError_t launch_router_route(const void* x, const void* wg, const float* bias, const void* w_sg,
+                               int64_t T, int E, int H, int k, void* logits, int32_t* idx,
+                               void* topw, float* sgate, int32_t* hist, int32_t* lrank,
+                               hipStream_t s) {
+  GroupWeights gw{};
+  gw.gate_up = wg;
+  gw.E = E;
+  gw.H = H;
+  const int nb = static_cast<int>((T + RouterShape128::kWT - 1) / RouterShape128::kWT);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const auto* ws = static_cast<const uint16_t*>(w_sg);
+  auto* lg = static_cast<uint16_t*>(logits);
+  auto* tw = static_cast<uint16_t*>(topw);
+  if (E <= 64)
+    router_route_kernel<8><<<round8(nb), kThreads, 0, s>>>(gw, xx, static_cast<int>(T), bias, ws, k,
+                                                           bits_of(E), nb, lg, idx, tw, sgate,
+                                                           hist, lrank);
+  else
+    router_route_kernel<16><<<round8(nb), kThreads, 0, s>>>(gw, xx, static_cast<int>(T), bias, ws,
+                                                            k, bits_of(E), nb, lg, idx, tw, sgate,
+                                                            hist, lrank);
+  return hipGetLastError();
+}
+
+hipError_t launch_scatter_build(const int32_t* idx, int64_t T, int k, const int32_t* base,
+                                const int32_t* counts, const int32_t* lrank, int32_t* offsets,
+                                int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,
+                                const GroupWeights& gw, bool shared, int max_tiles,
+                                int32_t* tiles, hipStream_t s) {
+  const int nb = static_cast<int>((T + RouterShape128::kWT - 1) / RouterShape128::kWT);
+  const int n_scatter = (nb * k + 15) / 16;
+  const int grid_gu = tiled_grid(gw, max_tiles, true), grid_dn = tiled_grid(gw, max_tiles, false);
+  const int blocks = build_blocks(max_tiles, grid_gu + grid_dn);
+  scatter_build_kernel<<<n_scatter + blocks, 1024, 0, s>>>(
+      idx, static_cast<int>(T), k, nb, base, counts, lrank, offsets, perm_tok, perm_slot, inv,
+      n_scatter, gw.E, shared ? 1 : 0, gw.sh_row0, max_tiles, Wide::kWT, Narrow::kWT, Tiny::kWT,
+      gw.I, gw.Is, gw.H, grid_gu, grid_dn, tiles);
   return hipGetLastError();
 }
 

@@ -151,6 +151,21 @@ def test_block_prefill_persistent_gate_up(gpu):
     gc.check_output(act.cpu().numpy(), ref.cpu().numpy(), gc.TOL_BF16)
 
 
+# Batches that select experts inside the tiled router (E <= 128, T >= 1024, tiled GEMMs):
+# 16 experts per lane (E = 128) under a Zipf bias, an expert count that is no multiple of 8
+# with a ragged last 64-token block, k > 8 (a lane's second slot), and a shared expert whose
+# gate the same kernel computes.
+@pytest.mark.parametrize("shape,T,zipf", [(MoEShape(1024, 128, 8, 256, 0), 2048, True),
+                                          (MoEShape(512, 100, 6, 256, 0), 1100, False),
+                                          (MoEShape(512, 96, 12, 256, 0), 1024, False),
+                                          (MoEShape(512, 80, 10, 256, 384), 1200, True)])
+def test_block_prefill_route_in_router(gpu, shape, T, zipf):
+    bias = None
+    if zipf:
+        bias = zipf_bias(torch.Generator().manual_seed(shape.num_experts), shape.num_experts)
+    _run_and_check(shape, T, gpu, seed=T, bias=bias, sample=96)
+
+
 def test_block_prefill_tiled_shared(gpu):
     """Tiled GEMMs with a shared expert of a different width (Is != I)."""
     shape = MoEShape(512, 16, 2, 256, 384)
