@@ -472,12 +472,12 @@ def main():
             "hit_experts": p["hit_experts"], "max_tokens_per_expert": p["max_tokens_per_expert"],
             "stage_us": {k_: round(v, 1) for k_, v in p["stage_us"].items()},
             "gate_up_tflops": round(pgf / (pgu * 1e-6) / 1e12, 2),
-            "roofline": {"kernel": "tiled_kernel<kGateUp>", "bound": "mfma",
+            "roofline": {"kernel": "tiled_persistent_kernel<kGateUp>", "bound": "mfma",
                          "achieved": round(pgf / (pgu * 1e-6) / 1e12, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s",
                          "frac": round(pgf / (pgu * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
                          "algorithmic_flops_per_launch": pgf, "avg_launch_us": round(pgu, 1),
-                         "traffic": (pmc_traffic("tiled_kernel<1>", PREFILL_TRAFFIC_FILE)
+                         "traffic": (pmc_traffic("tiled_persistent_kernel<1>", PREFILL_TRAFFIC_FILE)
                                      if default_prefill else None)},
             "cpu_baseline": None,
         }
