@@ -59,6 +59,27 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
   return v;
 }
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  v += dpp_f32<0x141>(v);
+  return v + dpp_f32<0x140>(v);
+}
+__device__ __forceinline__ float lane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Wave-wide maximum and sum on DPP (the 16-lane row reductions above, then the four row
+// results read from lanes 0, 16, 32, 48): a few cycles per step where a shuffle through LDS
+// takes a round trip. Every lane of the wave must be active. The sum adds in another order
+// than wave_sum.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = row16_sum(v);
+  return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
 
 // Activation quantisation (per row and 128 channels): scale = amax / 448, 1 for an all-zero
 // group; code = e4m3(value / scale). One group is held by 16 consecutive lanes of a wave

@@ -53,12 +53,12 @@ __device__ __forceinline__ void route_select(const float (&z)[EPL], int E, int k
     key[j] = e < E ? order_key(z[j]) : 0u;             // 0 is below every valid key
     m = fmaxf(m, z[j]);
   }
-  m = wave_max(m);
+  m = wave_max_dpp(m);
   float part = 0.f;
 #pragma unroll
   for (int j = 0; j < EPL; ++j)
     if (j * kWave + lane < E) part += expf(z[j] - m);
-  const float S = wave_sum(part);
+  const float S = wave_sum_dpp(part);
 
   // k rounds of argmax; lane r < k keeps round r's winner (expert and key)
   int my_e = 0;
@@ -95,7 +95,7 @@ __device__ __forceinline__ void route_select(const float (&z)[EPL], int E, int k
     const uint32_t u = (my_key & 0x80000000u) ? (my_key & 0x7fffffffu) : ~my_key;   // key -> z
     p = expf(__uint_as_float(u) - m) / S;
   }
-  const float psum = wave_sum(p);
+  const float psum = wave_sum_dpp(p);
   if (lane < k) {
     if (topw != nullptr) topw[o + lane] = static_cast<uint16_t>(f2bf(p / psum));
     if (idx_bytes == 8) reinterpret_cast<int64_t*>(idx_out)[o + lane] = my_e;
@@ -214,7 +214,7 @@ __device__ __forceinline__ void shared_gate(const uint16_t* __restrict__ x,
       d += bf_hi(a[q]) * bf_hi(b[q]);
     }
   }
-  d = round_bf(wave_sum(d));
+  d = round_bf(wave_sum_dpp(d));
   if (lane == 0) sgate[t] = 1.0f / (1.0f + expf(-d));
 }
 
