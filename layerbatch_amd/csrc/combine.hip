@@ -15,7 +15,9 @@ namespace lbmoe {
 // are read first, then every thread issues its row loads together before accumulating, so the
 // loads overlap. All loads are unconditional (indices past k or rows of dropped pairs read a
 // real entry and are masked afterwards): a load under a condition would make the compiler
-// wait for every earlier load at the join.
+// wait for every earlier load at the join. The expert-output rows are read once and y is
+// written once, both non-temporally, so neither stream displaces cached data (Qwen3-30B-A3B
+// T=8192: 58.8 -> 50.4 us; fp8 E=512 T=16384: 168 -> 147 us).
 constexpr int kCombineSlots = 8;   // slots whose row loads are in flight together
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       u32x4 o[kCombineSlots];
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i)
-        o[i] = ld16(rows + static_cast<int64_t>(max(p[i], 0)) * H + c);
+        o[i] = ld16_stream(rows + static_cast<int64_t>(max(p[i], 0)) * H + c);
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i) {
         const bool use = p[i] >= 0;        // dropped pairs and slots past k add nothing
@@ -55,7 +57,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     }
     if (sgate != nullptr) {
       const float g = sgate[t];
-      const u32x4 o = ld16(rows + static_cast<int64_t>(sh_row0 + t) * H + c);
+      const u32x4 o = ld16_stream(rows + static_cast<int64_t>(sh_row0 + t) * H + c);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         acc[2 * q] += g * bf_lo(o[q]);
@@ -65,7 +67,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     u32x4 pk;
 #pragma unroll
     for (int q = 0; q < 4; ++q) pk[q] = pack_bf2(acc[2 * q], acc[2 * q + 1]);
-    *reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + c) = pk;
+    __builtin_nontemporal_store(pk, reinterpret_cast<u32x4*>(y + static_cast<int64_t>(t) * H + c));
   }
 }
 
