@@ -337,7 +337,7 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
       }
     }
   } else {
-    store_staged<kCols, kWT>(lds, static_cast<uint16_t*>(dst), dst_ld, row0, r0, n, c0);
+    store_staged<kCols, kWT, true>(lds, static_cast<uint16_t*>(dst), dst_ld, row0, r0, n, c0);
   }
 }
 

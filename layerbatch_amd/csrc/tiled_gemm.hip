@@ -659,7 +659,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       }
     }
     ring_barrier();
-    store_staged<kCols, S::kWT>(lds, dst, dst_ld, row0, r0, n, c0);
+    store_staged<kCols, S::kWT, !GATEUP>(lds, dst, dst_ld, row0, r0, n, c0);   // down: read once
   } else if constexpr (STAGE) {
     // logits through LDS: staged rows, then whole rows stored with 16-byte lanes
     constexpr int kStride = kStagedLogitStride<S>;
