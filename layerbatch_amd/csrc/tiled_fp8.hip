@@ -166,13 +166,15 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
 #pragma unroll
     for (int t = 0; t < kN16; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // narrow and tiny tiles' weight copies are non-temporal, as in the bf16 kernel
+  constexpr int kWeightPolicy = S::kWT < kWM ? 2 : 0;
   auto issue = [&](int stage, int k0) {
     u32x4* buf = lds + stage * kStageU4;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
       __builtin_amdgcn_global_load_lds(abase[i] + (aoff[i] + static_cast<uint32_t>(k0)),
                                        (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
-                                       16, 0, 0);
+                                       16, 0, kWeightPolicy);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
       __builtin_amdgcn_global_load_lds(src + (boff[i] + static_cast<uint32_t>(k0)),
