@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LBMOE_ABI_VERSION 1
+#define LBMOE_ABI_VERSION 2
 
 typedef enum lbmoe_status {
   LBMOE_OK = 0,
@@ -75,6 +75,15 @@ typedef struct lbmoe_layer {
   const float* shared_gate_scale;   /* fp8 only: fp32 [Is/128,H/128]                     */
   const float* shared_up_scale;     /* fp8 only: fp32 [Is/128,H/128]                     */
   const float* shared_down_scale;   /* fp8 only: fp32 [H/128,Is/128]                     */
+  /* Optional, bf16 layers only (NULL: not used): copies of the expert weights in the tiled
+   * layout that lbmoe_pack_weights writes. Each one that is set replaces its checkpoint tensor
+   * in the prefill-sized GEMMs, which stream it markedly faster; the checkpoint tensors stay
+   * required (decode-sized batches read them). No counterpart in the reference: the module's
+   * parameters are the checkpoint tensors, and these are derived from them once. */
+  const void*  gate_up_tiled;        /* from gate_up_proj, same bytes                     */
+  const void*  down_tiled;           /* from down_proj, same bytes                        */
+  const void*  shared_gate_up_tiled; /* from shared gate_proj + up_proj, 2*Is*H bf16      */
+  const void*  shared_down_tiled;    /* from shared down_proj, same bytes                 */
 } lbmoe_layer;
 
 /* Human-readable name of a status code (static string). */
@@ -121,6 +130,19 @@ int32_t lbmoe_forward_norm(const lbmoe_layer* layer, const void* hidden, const v
                            const void* norm_weight, float eps, int64_t T, void* y,
                            void* residual_out, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/*
+ * Writes the tiled copies of a bf16 layer's expert weights (the lbmoe_layer *_tiled fields)
+ * from its checkpoint tensors: gate_up_tiled and down_tiled (as many bytes as gate_up_proj and
+ * down_proj), and, with a shared expert, shared_gate_up_tiled (2*Is*H bf16) and
+ * shared_down_tiled (H*Is bf16). Run once after the weights are loaded (or changed); the copies
+ * are device memory the caller owns and must not overlap the checkpoint tensors. Shapes the
+ * prefill GEMMs do not tile (H not a multiple of 256) return LBMOE_ERR_SHAPE, fp8 layers
+ * LBMOE_ERR_DTYPE. No counterpart in the reference (a load-time layout step, like the fp8
+ * quantisation of lbmoe_quantize_fp8_blocks).
+ */
+int32_t lbmoe_pack_weights(const lbmoe_layer* layer, void* gate_up_tiled, void* down_tiled,
+                           void* shared_gate_up_tiled, void* shared_down_tiled, void* stream);
 
 /* Bytes of the device workspace lbmoe_forward_static uses (one per GPU, held until the process
  * ends). */

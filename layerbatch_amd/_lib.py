@@ -41,6 +41,8 @@ class LbmoeLayer(ctypes.Structure):
         ("shared_gate_proj", _p), ("shared_up_proj", _p), ("shared_down_proj", _p),
         ("shared_expert_gate", _p),
         ("shared_gate_scale", _p), ("shared_up_scale", _p), ("shared_down_scale", _p),
+        ("gate_up_tiled", _p), ("down_tiled", _p),
+        ("shared_gate_up_tiled", _p), ("shared_down_tiled", _p),
     ]
 
 
@@ -52,6 +54,7 @@ _SIGS = {
     "lbmoe_workspace_size": (_i32, [_PL, _i64, ctypes.POINTER(_sz)]),
     "lbmoe_workspace_region": (_i32, [_PL, _i64, _i32, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "lbmoe_forward": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p]),
+    "lbmoe_pack_weights": (_i32, [_PL, _p, _p, _p, _p, _p]),
     "lbmoe_forward_profiled": (_i32, [_PL, _p, _i64, _p, _p, _sz, _p, ctypes.POINTER(_p), _i32]),
     "lbmoe_forward_static": (_i32, [_PL, _p, _i64, _p, _p]),
     "lbmoe_forward_norm": (_i32, [_PL, _p, _p, _p, ctypes.c_float, _i64, _p, _p, _p, _sz, _p]),

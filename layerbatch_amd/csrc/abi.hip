@@ -132,6 +132,10 @@ static GroupWeights group_weights(const lbmoe_layer& L, bool with_shared, int64_
   g.sh_gate_scale = L.shared_gate_scale;
   g.sh_up_scale = L.shared_up_scale;
   g.sh_down_scale = L.shared_down_scale;
+  g.gate_up_tiled = L.gate_up_tiled;
+  g.down_tiled = L.down_tiled;
+  g.sh_gate_up_tiled = L.shared_gate_up_tiled;
+  g.sh_down_tiled = L.shared_down_tiled;
   g.E = L.num_experts;
   g.H = L.hidden_size;
   g.I = L.moe_intermediate_size;
@@ -160,7 +164,8 @@ static P* at(void* ws, const WsLayout& w, int r) {
 constexpr double kTiledMinTokensPerExpert = 28.0;
 
 static bool use_tiled(const GroupWeights& gw, int64_t T, int k) {
-  return tiled_supported(gw) && static_cast<double>(T) * k / gw.E >= kTiledMinTokensPerExpert;
+  return tiled_supported(gw) && tiled_offsets_fit(gw, T, k) &&
+         static_cast<double>(T) * k / gw.E >= kTiledMinTokensPerExpert;
 }
 
 // Routed experts of one call: permute, gate_up, down, combine.
@@ -311,7 +316,40 @@ int32_t lbmoe_check_layer(const lbmoe_layer* layer) {
   const lbmoe_layer& L = *layer;
   if (!L.gate_weight) return LBMOE_ERR_NULL;
   if ((st = check_expert_ptrs(L)) != LBMOE_OK) return st;
+  if (is_fp8(L) && (L.gate_up_tiled || L.down_tiled || L.shared_gate_up_tiled ||
+                    L.shared_down_tiled))
+    return LBMOE_ERR_DTYPE;             // the tiled copies are bf16 layouts
   if (L.shared_intermediate_size > 0) return check_shared_ptrs(L);
+  return LBMOE_OK;
+}
+
+int32_t lbmoe_pack_weights(const lbmoe_layer* layer, void* gate_up_tiled, void* down_tiled,
+                           void* shared_gate_up_tiled, void* shared_down_tiled, void* stream) {
+  int32_t st = lbmoe_check_layer(layer);
+  if (st != LBMOE_OK) return st;
+  const lbmoe_layer& L = *layer;
+  if (is_fp8(L)) return LBMOE_ERR_DTYPE;
+  const bool sh = L.shared_intermediate_size > 0;
+  if (!gate_up_tiled || !down_tiled || (sh && (!shared_gate_up_tiled || !shared_down_tiled)))
+    return LBMOE_ERR_NULL;
+  if (!tiled_supported(group_weights(L, sh, 0))) return LBMOE_ERR_SHAPE;
+  if ((st = check_device()) != LBMOE_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int E = L.num_experts, H = L.hidden_size, I = L.moe_intermediate_size;
+  const int Is = L.shared_intermediate_size;
+  const auto* gu = static_cast<const uint16_t*>(L.gate_up_proj);
+  LBMOE_TRY(launch_pack_tiled(gu, gu + static_cast<int64_t>(I) * H, int64_t{2} * I * H, E, I, H,
+                              true, static_cast<uint16_t*>(gate_up_tiled), s));
+  LBMOE_TRY(launch_pack_tiled(static_cast<const uint16_t*>(L.down_proj), nullptr,
+                              static_cast<int64_t>(H) * I, E, H, I, false,
+                              static_cast<uint16_t*>(down_tiled), s));
+  if (sh) {
+    LBMOE_TRY(launch_pack_tiled(static_cast<const uint16_t*>(L.shared_gate_proj),
+                                static_cast<const uint16_t*>(L.shared_up_proj), 0, 1, Is, H, true,
+                                static_cast<uint16_t*>(shared_gate_up_tiled), s));
+    LBMOE_TRY(launch_pack_tiled(static_cast<const uint16_t*>(L.shared_down_proj), nullptr, 0, 1,
+                                H, Is, false, static_cast<uint16_t*>(shared_down_tiled), s));
+  }
   return LBMOE_OK;
 }
 

@@ -54,6 +54,11 @@ struct GroupWeights {
   const float* sh_gate_scale;
   const float* sh_up_scale;
   const float* sh_down_scale;
+  // optional bf16 copies in the LDS-tiled GEMMs' tiled layout (pack_tiled_kernel), or null
+  const void* gate_up_tiled;     // [E][I/128][H/64][256 x 64]
+  const void* down_tiled;        // [E][H/256][I/64][256 x 64]
+  const void* sh_gate_up_tiled;  // [Is/128][H/64][256 x 64]
+  const void* sh_down_tiled;     // [H/256][Is/64][256 x 64]
   int E, H, I, Is;
   int g0, groups;
   int sh_row0;
@@ -210,6 +215,9 @@ int tiled_max_tiles(int64_t rows, int groups);  // rows = routed + shared
 // Bytes of a tile list with max_tiles entries and the dispatch tables of both GEMMs.
 int64_t tiled_list_bytes(int max_tiles, int I, int Is, int H);
 bool tiled_supported(const GroupWeights& gw);
+// Whether every byte offset of the bf16 tiled GEMMs' buffer copies stays below 2^31 for a call
+// of T tokens (x, the act rows of the routed and shared experts, one expert's weight matrix).
+bool tiled_offsets_fit(const GroupWeights& gw, int64_t T, int k);
 // rows = routed + shared rows of the call
 bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows);
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,
@@ -218,6 +226,13 @@ hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, con
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,
                                 void* act, hipStream_t s);
+// Writes the tiled layout of bf16 weights for the LDS-tiled GEMMs. gate_up: gate and up are
+// [C, K] row blocks (C channels) of `groups` groups, group_stride elements apart, written as
+// [groups][C/128][K/64] blocks; otherwise w [C, K] (C output rows) as [groups][C/256][K/64].
+// dst holds as many elements as the source tensors.
+hipError_t launch_pack_tiled(const uint16_t* gate, const uint16_t* up, int64_t group_stride,
+                             int groups, int C, int K, bool gate_up, uint16_t* dst,
+                             hipStream_t s);
 hipError_t launch_down_tiled(const GroupWeights& gw, const void* act, int act_ld,
                              const int32_t* tiles, int max_tiles, int64_t T, void* out,
                              hipStream_t s);

@@ -300,7 +300,9 @@ static hipError_t launch_router_decode(const uint16_t* x, const NormIn& nm, cons
 constexpr int64_t kTiledRouterMinTokens = 1024;
 
 bool router_is_tiled(int64_t T, int E, int H) {
-  return T >= kTiledRouterMinTokens && tiled_router_supported(E, H);
+  // the tiled router's buffer copies address x and the gate weight with byte offsets < 2^31
+  return T >= kTiledRouterMinTokens && tiled_router_supported(E, H) &&
+         T * H * 2 < (int64_t{1} << 31);
 }
 
 hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E, int H,

@@ -37,6 +37,17 @@ __device__ __forceinline__ void wait_ring(int later) {
   }
 }
 
+// Buffer resource for raw accesses (stride 0, no swizzle) at byte offsets below 2^31 from
+// `base`, which must be wave-uniform; readfirstlane makes that visible to the compiler, so the
+// descriptor lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, 0x7fffffff, 0x00020000);
+}
+
 // Workgroup b runs on XCD b % 8. The first `items` work items are spread over the 8 XCDs in
 // contiguous chunks, so consecutive items (which share operands) run together on one XCD's L2
 // and every XCD gets an equal share however much larger than `items` the grid is. Returns the

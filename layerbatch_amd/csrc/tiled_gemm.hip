@@ -31,8 +31,14 @@
 // four consecutive output channels of one token are stored together. LDS rows are kBK bf16 in
 // 16-byte chunks; chunk j of row r is stored at a row-dependent XOR of j (swz), which keeps
 // the 32-row MFMA operand reads free of bank conflicts.
-// Gate_up workgroups take kWM/2 channels: the weight rows of wave row-block h are the gate rows
-// then the up rows of the same channels, so SiLU*mul pairs accumulators in registers.
+// Gate_up workgroups take kWM/2 channels: the weight rows alternate in 32-row blocks between
+// the gate and the up rows of the same 32 channels, so SiLU*mul pairs accumulators in registers.
+//
+// Weights come either in the checkpoint layout ([E,2I,H], [E,H,I]) or, when the caller has
+// packed them (lbmoe_pack_weights -> pack_tiled_kernel), in a tiled layout where each k-tile of
+// a weight tile is one contiguous 32 KB block already in LDS order. HBM streams those blocks
+// markedly faster than 256 row segments of 128 bytes spread over 1 MB (a read probe in the
+// ring's pattern, with token copies that hit L2 as here: 6.7 against 5.2 TB/s).
 #include "common.hpp"
 #include "internal.hpp"
 #include "route_token.hpp"
@@ -397,7 +403,14 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
 
   // Direct global->LDS copies: wave copy i writes one contiguous 1 KB LDS block of
   // kRowsPerLoad rows; lane l fills slot l of it, i.e. row R0 + l/kChunks at swizzled position
-  // l%kChunks, so it fetches the chunk that the swizzle places there.
+  // l%kChunks, so it fetches the chunk that the swizzle places there. The copies go through
+  // buffer resources (buffer_load ... lds): a wave-uniform descriptor per copy, a fixed 32-bit
+  // byte offset per lane, and the k-tile's step in the scalar offset. With global_load_lds the
+  // compiler counted the copies as LDS operations as well and then waited for every
+  // outstanding LDS read (lgkmcnt(0)) before each k-step's first MFMA; buffer copies leave the
+  // LDS reads in order for it, so each MFMA waits only for its own fragments. Byte offsets stay
+  // below 2^31 (tiled_offsets_fit on the host).
+  static_assert(32 % kRowsPerLoad == 0, "a copy's rows lie in one 32-row block");
   const uint16_t* wbase;
   const uint16_t* wup = nullptr;
   if (GATEUP) {
@@ -415,26 +428,50 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
                    : static_cast<const uint16_t*>(gw.down) + static_cast<int64_t>(g) * H * gw.I;
   }
   const int lrow = lane / kChunks, lpos = lane % kChunks;
-  const uint16_t* ap[kALoads];
+  __amdgpu_buffer_rsrc_t ars[kALoads];
+  uint32_t aoff[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
-    const int row = (w * kALoads + i) * kRowsPerLoad + lrow;    // local weight row
+    const int row0c = (w * kALoads + i) * kRowsPerLoad;          // the copy's first row (uniform)
+    const int row = row0c + lrow;                                // local weight row
     const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
     int grow;
     const uint16_t* base = wbase;
     if (GATEUP) {
-      // wave h's rows: the gate rows then the up rows of channels c0 + h*kRW/2 .. +kRW/2
-      const int half = row / kRW, sub = row % kRW;
-      base = sub < kRW / 2 ? wbase : wup;
-      grow = c0 + half * (kRW / 2) + (sub % (kRW / 2));
+      // 32-row blocks alternate the gate and the up rows of 32 channels: block b holds channels
+      // c0 + 32 (b / 2) .. +32, gate rows for even b, up rows for odd b, so MFMA tiles 2p and
+      // 2p + 1 of a wave pair up in every tile shape
+      base = ((row0c >> 5) & 1) ? wup : wbase;
+      grow = c0 + 32 * (row >> 6) + (row & 31);
     } else if (ROUTER) {
       grow = min(c0 + row, gw.E - 1);      // rows past E repeat a valid row; not stored
     } else {
       grow = c0 + row;
     }
-    ap[i] = base + static_cast<int64_t>(grow) * K + 8 * j;
+    ars[i] = raw_rsrc(base);
+    aoff[i] = static_cast<uint32_t>((static_cast<int64_t>(grow) * K + 8 * j) * 2);
   }
-  const uint16_t* bp[kBLoads];
+  // Weight bytes between k-tile kt and kt + 1 of a copy: kBK elements along the checkpoint
+  // rows, or one whole k-tile block in the tiled layout (pack_tiled_kernel), where the kWM x
+  // kBK k-tile is a contiguous 32 KB block in LDS order, so wave copy i reads the 1 KB at slot
+  // (w * kALoads + i) * 64 of it, lane l the 16 bytes of slot l.
+  int astep = kBK * 2;
+  if constexpr (!ROUTER) {
+    const void* tl = GATEUP ? (shared ? gw.sh_gate_up_tiled : gw.gate_up_tiled)
+                            : (shared ? gw.sh_down_tiled : gw.down_tiled);
+    if (tl != nullptr) {
+      const int64_t group = shared ? 0 : static_cast<int64_t>(g) * (GATEUP ? 2 : 1) * Ig * H;
+      const uint16_t* wtl = static_cast<const uint16_t*>(tl) + group + static_cast<int64_t>(wt) * kWM * K;
+      astep = kWM * kBK * 2;
+#pragma unroll
+      for (int i = 0; i < kALoads; ++i) {
+        ars[i] = raw_rsrc(wtl);
+        aoff[i] = static_cast<uint32_t>(((w * kALoads + i) * (kRowsPerLoad * kChunks) + lane) * 16);
+      }
+    }
+  }
+  const __amdgpu_buffer_rsrc_t brs = raw_rsrc(src);
+  uint32_t boff[kBLoads];
 #pragma unroll
   for (int i = 0; i < kBLoads; ++i) {
     const int lt = (w * kBLoads + i) * kRowsPerLoad + lrow;     // local token
@@ -442,7 +479,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     const int j = lpos ^ ((row >> kSwzShift) & (kChunks - 1));
     const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
     const int srow = ROUTER ? p : (GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p);
-    bp[i] = src + static_cast<int64_t>(srow) * src_ld + 8 * j;
+    boff[i] = static_cast<uint32_t>((static_cast<int64_t>(srow) * src_ld + 8 * j) * 2);
   }
 
   f32x16 acc[kMT][kNT];
@@ -459,25 +496,26 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   // and wide-tile weights that are reused (E=512 T=4096 layer 755 -> 727 us, Qwen3-30B-A3B
   // T=8192 Zipf 763 -> 741 us; the same for every tile was slower, 766 -> 799 us).
   constexpr int kWeightPolicy = (!ROUTER && S::kWT < kWM) ? 2 : 0;
-  auto issue_a = [&](int stage, int k0) {
+  // the copies of k-tile kt into ring stage `stage`
+  auto issue_a = [&](int stage, int kt) {
     u32x4* buf = lds + S::a_off(stage);
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
-      __builtin_amdgcn_global_load_lds(ap[i] + k0,
-                                       (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
-                                       16, 0, kWeightPolicy);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ars[i], (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks), 16, aoff[i],
+          kt * astep, 0, kWeightPolicy);
   };
-  auto issue_b = [&](int stage, int k0) {
+  auto issue_b = [&](int stage, int kt) {
     u32x4* buf = lds + S::b_off(stage);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
-      __builtin_amdgcn_global_load_lds(bp[i] + k0,
-                                       (lds_ptr)(buf + ((w * kBLoads + i) * kRowsPerLoad) * kChunks),
-                                       16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          brs, (lds_ptr)(buf + ((w * kBLoads + i) * kRowsPerLoad) * kChunks), 16, boff[i],
+          kt * (kBK * 2), 0, 0);
   };
-  auto issue = [&](int stage, int k0) {
-    issue_a(stage, k0);
-    issue_b(stage, k0);
+  auto issue = [&](int stage, int kt) {
+    issue_a(stage, kt);
+    issue_b(stage, kt);
   };
 
   // Ring protocol (the asymmetric ring issues A0 B0 A1 B1 A2 up front, then refills B kt+2
@@ -492,23 +530,25 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   if constexpr (S::kAsym) {
 #pragma unroll
     for (int st = 0; st < kStages; ++st) {
-      if (st < nk) issue_a(st, st * kBK);
-      if (st < S::kBStages && st < nk) issue_b(st, st * kBK);
+      if (st < nk) issue_a(st, st);
+      if (st < S::kBStages && st < nk) issue_b(st, st);
     }
   } else {
 #pragma unroll
     for (int st = 0; st < kStages; ++st)
-      if (st < nk) issue(st, st * kBK);
+      if (st < nk) issue(st, st);
   }
   const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
   auto read_frags = [&](int kt, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
     const int j = 2 * ks + mk;
     const u32x4* ca = lds + S::a_off(kt % kStages);
     const u32x4* cb = lds + S::b_off(kt % S::kBStages);
-#pragma unroll
-    for (int i = 0; i < kMT; ++i) fa[i] = ca[S::swz(wm * kRW + 32 * i + mr, j)];
+    // token fragments first: every MFMA of the k-step needs one, so the next k-step's first
+    // MFMA then waits only for the oldest reads, not for the whole batch
 #pragma unroll
     for (int t = 0; t < kNT; ++t) fb[t] = cb[S::swz(wn * (kNT * 32) + 32 * t + mr, j)];
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) fa[i] = ca[S::swz(wm * kRW + 32 * i + mr, j)];
   };
   auto mfma_all = [&](const u32x4 (&fa)[kMT], const u32x4 (&fb)[kNT]) {
 #pragma unroll
@@ -557,10 +597,10 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       ring_barrier();
       read_frags(kt + 1, 0, fa[0], fb[0]);
       if constexpr (S::kAsym) {
-        if constexpr (REFILL >= 1) issue_b(kt % S::kBStages, (kt + S::kBStages) * kBK);
-        if constexpr (REFILL >= 2) issue_a(kt % kStages, (kt + kStages) * kBK);
+        if constexpr (REFILL >= 1) issue_b(kt % S::kBStages, kt + S::kBStages);
+        if constexpr (REFILL >= 2) issue_a(kt % kStages, kt + kStages);
       } else {
-        if constexpr (REFILL >= 2) issue(kt % kStages, (kt + kStages) * kBK);
+        if constexpr (REFILL >= 2) issue(kt % kStages, kt + kStages);
       }
       if constexpr (CLAIM) {
         // Every copy has landed (the wait above), so no ring wait counts the atomic. Through an
@@ -645,7 +685,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
           float a[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            a[v] = GATEUP ? silu(acc[i][t][4 * v4 + v]) * acc[i + kMT / 2][t][4 * v4 + v]
+            a[v] = GATEUP ? silu(acc[2 * i][t][4 * v4 + v]) * acc[2 * i + 1][t][4 * v4 + v]
                           : acc[i][t][4 * v4 + v];
           const int c = (GATEUP ? wm * (kRW / 2) : wm * kRW) + 32 * i + 8 * v4 + rq;
           *reinterpret_cast<u32x2*>(st + staged_slot<kCols>(r, c / 8) * 16 + (c % 8) * 2) =
@@ -890,11 +930,68 @@ int tiled_max_tiles(int64_t rows, int groups) {
   return static_cast<int>(rows / Wide::kWT) + groups * ((Wide::kWT - Narrow::kWT) / Narrow::kWT) + 1;
 }
 
+// ---- tiled weight layout -----------------------------------------------------------------
+// One k-tile block = kWM weight rows x kBK bf16 of one weight tile, 2048 16-byte slots in the
+// LDS order of the ring: slot s holds chunk (s % 8) ^ f(s / 8) of tile row s / 8 (the swizzle
+// of the tile shapes). Tile rows follow tile_product: for gate_up, 32-row blocks alternate the
+// gate and the up rows of 32 channels (tile wt: channels 128 wt ..); for down, tile wt holds
+// output rows 256 wt ... Blocks run k-tile by k-tile within a tile, tile by tile within a
+// group. One thread per slot; reads are 16-byte row chunks, writes are contiguous.
+static_assert(Wide::kBK == Narrow::kBK && Wide::kBK == Tiny::kBK, "one tiled layout for every shape");
+static_assert(Wide::kRows == kWM && Narrow::kRows == kWM && Tiny::kRows == kWM, "kWM-row weight tiles");
+constexpr int kPackSlots = kWM * Wide::kChunks;    // 16-byte slots per k-tile block
+__global__ __launch_bounds__(256) void pack_tiled_kernel(const uint16_t* __restrict__ gate,
+                                                         const uint16_t* __restrict__ up,
+                                                         int64_t group_stride, int64_t total,
+                                                         int tiles, int K, int gate_up,
+                                                         uint16_t* __restrict__ dst) {
+  const int nk = K / Wide::kBK;
+  for (int64_t i = blockIdx.x * int64_t{256} + threadIdx.x; i < total;
+       i += int64_t{256} * gridDim.x) {
+    const int slot = static_cast<int>(i % kPackSlots);
+    const int64_t blk = i / kPackSlots;
+    const int kt = static_cast<int>(blk % nk);
+    const int wt = static_cast<int>((blk / nk) % tiles);
+    const int64_t grp = blk / nk / tiles;
+    const int r = slot / Wide::kChunks;
+    const int j = (slot % Wide::kChunks) ^ ((r >> Wide::kSwzShift) & (Wide::kChunks - 1));
+    const uint16_t* srow;
+    if (gate_up) {
+      const int b = r >> 5;
+      const int ch = wt * (kWM / 2) + 32 * (b >> 1) + (r & 31);
+      srow = ((b & 1) ? up : gate) + grp * group_stride + static_cast<int64_t>(ch) * K;
+    } else {
+      srow = gate + grp * group_stride + static_cast<int64_t>(wt * kWM + r) * K;
+    }
+    *reinterpret_cast<u32x4*>(dst + i * 8) = ld16(srow + kt * Wide::kBK + 8 * j);
+  }
+}
+
+hipError_t launch_pack_tiled(const uint16_t* gate, const uint16_t* up, int64_t group_stride,
+                             int groups, int C, int K, bool gate_up, uint16_t* dst,
+                             hipStream_t s) {
+  const int rows_per_tile = gate_up ? kWM / 2 : kWM;
+  const int tiles = C / rows_per_tile;
+  const int64_t total = static_cast<int64_t>(groups) * tiles * (K / Wide::kBK) * kPackSlots;
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = (total + 255) / 256;
+  pack_tiled_kernel<<<static_cast<unsigned>(blocks < 65536 ? blocks : 65536), 256, 0, s>>>(
+      gate, up, group_stride, total, tiles, K, gate_up ? 1 : 0, dst);
+  return hipGetLastError();
+}
+
 bool tiled_supported(const GroupWeights& gw) {
   constexpr int kBKmax = Wide::kBK > Narrow::kBK ? Wide::kBK : Narrow::kBK;
   return gw.H % kWM == 0 && gw.H % kBKmax == 0 && gw.I % (kWM / 2) == 0 &&
          (gw.Is == 0 || gw.Is % (kWM / 2) == 0) && gw.I % kBKmax == 0 &&
          (gw.Is == 0 || gw.Is % kBKmax == 0) && gw.I < (1 << 20) && gw.E < (1 << 16) - 1;
+}
+
+bool tiled_offsets_fit(const GroupWeights& gw, int64_t T, int k) {
+  constexpr int64_t kMax = int64_t{1} << 31;
+  const int64_t imax = gw.I > gw.Is ? gw.I : gw.Is;
+  return T * gw.H * 2 < kMax && T * (k + 1) * imax * 2 < kMax &&
+         static_cast<int64_t>(imax) * gw.H * 2 < kMax;
 }
 
 // Workgroups of a bf16 GEMM launch: one per possible item; the per-XCD rounding of the two item

@@ -177,6 +177,7 @@ class Qwen3_5Experts(nn.Module):
             torch.empty(num_experts, hidden_size, moe_intermediate_size))
         self.weight_dtype = _lib.LBMOE_W_BF16
         self.gate_up_q = self.gate_up_scale = self.down_q = self.down_scale = None
+        self.gate_up_tiled = self.down_tiled = None     # pack_tiled_ copies (bf16 only)
 
     def fill_layer(self, L):
         L.num_experts = self.num_experts
@@ -196,6 +197,9 @@ class Qwen3_5Experts(nn.Module):
             _require_shape(self.down_proj, (E, H, I), "experts.down_proj")
             L.gate_up_proj = self.gate_up_proj.data_ptr()
             L.down_proj = self.down_proj.data_ptr()
+            if self.gate_up_tiled is not None:
+                L.gate_up_tiled = self.gate_up_tiled.data_ptr()
+                L.down_tiled = self.down_tiled.data_ptr()
 
     def forward(self, hidden_states, top_k_indices, top_k_weights):
         _require(hidden_states, "hidden_states", ndim=2)
@@ -234,6 +238,7 @@ class Qwen3_5SharedExpertMLP(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
         self.weight_dtype = _lib.LBMOE_W_BF16
         self.q = None   # fp8: dict name -> (codes, scales)
+        self.gate_up_tiled = self.down_tiled = None     # pack_tiled_ copies (bf16 only)
 
     def _ptrs(self):
         if self.weight_dtype == _lib.LBMOE_W_FP8_E4M3:
@@ -253,6 +258,9 @@ class Qwen3_5SharedExpertMLP(nn.Module):
         (g, u, d), (gs, us, ds) = self._ptrs()
         L.shared_gate_proj, L.shared_up_proj, L.shared_down_proj = g, u, d
         L.shared_gate_scale, L.shared_up_scale, L.shared_down_scale = gs, us, ds
+        if self.weight_dtype == _lib.LBMOE_W_BF16 and self.gate_up_tiled is not None:
+            L.shared_gate_up_tiled = self.gate_up_tiled.data_ptr()
+            L.shared_down_tiled = self.down_tiled.data_ptr()
 
     def forward(self, x):
         _require(x, "x", ndim=2)
@@ -380,6 +388,38 @@ class Qwen3_5SparseMoeBlock(nn.Module):
         return y, new_residual
 
     @torch.no_grad()
+    def pack_tiled_(self):
+        """Derive the tiled copies of the bf16 expert weights (lbmoe_pack_weights), which the
+        prefill-sized GEMMs stream faster than the checkpoint tensors; forward then passes both.
+        The copies hold as many bytes as the expert weights again and are not updated when the
+        weights change: call this again after loading new weights. No counterpart in the
+        reference (a load-time layout step)."""
+        if self.experts.weight_dtype != _lib.LBMOE_W_BF16:
+            raise RuntimeError("pack_tiled_ needs bf16 expert weights")
+        ex, se = self.experts, self.shared_expert
+        ex.gate_up_tiled = ex.down_tiled = None
+        if se is not None:
+            se.gate_up_tiled = se.down_tiled = None
+        L = self.layer()
+        gu, dn = torch.empty_like(ex.gate_up_proj), torch.empty_like(ex.down_proj)
+        sgu = sdn = None
+        if se is not None:
+            Is, H = se.gate_proj.weight.shape
+            sgu = torch.empty((2 * Is, H), dtype=se.gate_proj.weight.dtype,
+                              device=se.gate_proj.weight.device)
+            sdn = torch.empty_like(se.down_proj.weight)
+        dev = gu.device
+        with torch.cuda.device(dev):
+            check(lib().lbmoe_pack_weights(ctypes.byref(L), ptr(gu), ptr(dn),
+                                           ptr(sgu) if sgu is not None else None,
+                                           ptr(sdn) if sdn is not None else None,
+                                           _lib.stream_of(dev)), "lbmoe_pack_weights")
+        ex.gate_up_tiled, ex.down_tiled = gu, dn
+        if se is not None:
+            se.gate_up_tiled, se.down_tiled = sgu, sdn
+        return self
+
+    @torch.no_grad()
     def quantize_fp8_(self):
         """Convert expert (and shared-expert) weights to e4m3fn + 128x128 block scales."""
         ex = self.experts
@@ -420,6 +460,7 @@ class Qwen3_5SparseMoeBlock(nn.Module):
         ex.gate_up_q, ex.gate_up_scale = codes_scales(gu_q, gu_s, (E, 2 * I, H), "experts.gate_up_proj")
         ex.down_q, ex.down_scale = codes_scales(d_q, d_s, (E, H, I), "experts.down_proj")
         ex.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+        ex.gate_up_tiled = ex.down_tiled = None        # bf16 layouts: no longer valid
         if self.shared_expert is not None:
             if shared is None:
                 raise RuntimeError("this block has a shared expert: its fp8 weights are required")
@@ -429,4 +470,5 @@ class Qwen3_5SparseMoeBlock(nn.Module):
             se.q = {n: codes_scales(*shared[n], shapes[n], f"shared_expert.{n}_proj.weight")
                     for n in ("gate", "up", "down")}
             se.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+            se.gate_up_tiled = se.down_tiled = None
         return self

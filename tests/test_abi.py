@@ -27,7 +27,7 @@ def test_library_exports_every_declared_entry_point(lbmoe):
     for n in names:
         assert hasattr(lbmoe, n), n
     assert set(names) == set(_lib.EXPORTED), "ctypes signatures out of sync with the header"
-    assert lbmoe.lbmoe_abi_version() == 1
+    assert lbmoe.lbmoe_abi_version() == 2
 
 
 def test_struct_layout_matches_header(tmp_path):
@@ -128,6 +128,26 @@ def test_forward_rejects_bad_arguments_before_any_device_call(lbmoe):
     assert lbmoe.lbmoe_quantize_fp8_blocks(p, 2, 100, 128, p, p, None) == ERR_SHAPE
     assert lbmoe.lbmoe_quantize_fp8_blocks(None, 2, 128, 128, p, p, None) == ERR_NULL
     assert lbmoe.lbmoe_dense_mlp(p, p, p, None, None, None, 1024, 0, 0, p, 4, p, p, 1 << 20, None) == ERR_SHAPE
+
+
+def test_pack_weights_rejects_bad_arguments_before_any_device_call(lbmoe):
+    p = ctypes.c_void_p(0x10000)
+    L = _layer()
+    assert lbmoe.lbmoe_pack_weights(None, p, p, None, None, None) == ERR_NULL
+    assert lbmoe.lbmoe_pack_weights(ctypes.byref(L), None, p, None, None, None) == ERR_NULL
+    assert lbmoe.lbmoe_pack_weights(ctypes.byref(L), p, None, None, None, None) == ERR_NULL
+    Ls = _layer(shared_intermediate_size=512, shared_gate_proj=1, shared_up_proj=1,
+                shared_down_proj=1, shared_expert_gate=1)
+    assert lbmoe.lbmoe_pack_weights(ctypes.byref(Ls), p, p, None, p, None) == ERR_NULL
+    # H a multiple of 128 but not of the 256-row weight tiles: not tiled, nothing to pack
+    assert lbmoe.lbmoe_pack_weights(ctypes.byref(_layer(hidden_size=1152)), p, p, None, None,
+                                    None) == ERR_SHAPE
+    Lf = _layer(weight_dtype=1, gate_up_scale=1, down_scale=1)
+    assert lbmoe.lbmoe_pack_weights(ctypes.byref(Lf), p, p, None, None, None) == ERR_DTYPE
+    # tiled copies are bf16 layouts: an fp8 layer that names one is rejected
+    assert lbmoe.lbmoe_check_layer(ctypes.byref(_layer(weight_dtype=1, gate_up_scale=1,
+                                                       down_scale=1, down_tiled=1))) == ERR_DTYPE
+    assert lbmoe.lbmoe_check_layer(ctypes.byref(_layer(gate_up_tiled=1, down_tiled=1))) == OK
 
 
 def test_status_strings(lbmoe):

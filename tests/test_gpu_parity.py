@@ -40,11 +40,14 @@ def _region(blk, ws, T, name, dtype, shape):
     return ws[off:off + n * esz].view(dtype).view(shape)
 
 
-def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu", sample=None):
+def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu", sample=None,
+                   pack=False):
     w, g = make_layer(shape, seed=seed, device=gen_device)
     x = make_x(g, T, shape.hidden_size, device=gen_device)
     wd = {k_: v.to(device) for k_, v in w.items()}
     blk = _block(shape, wd, device)
+    if pack:
+        blk.pack_tiled_()
     if bias is not None:
         blk.gate.logit_bias = bias.to(device)
     xd = x.to(device)
@@ -164,6 +167,31 @@ def test_block_prefill_route_in_router(gpu, shape, T, zipf):
     if zipf:
         bias = zipf_bias(torch.Generator().manual_seed(shape.num_experts), shape.num_experts)
     _run_and_check(shape, T, gpu, seed=T, bias=bias, sample=96)
+
+
+# Tiled-layout copies of the expert weights (lbmoe_pack_weights): the prefill GEMMs read them
+# instead of the checkpoint tensors and give the same output bit for bit, and the oracle agrees.
+# Cases: the router-fused path under a Zipf bias (wide, narrow and tiny tiles), a shared expert
+# narrower than the routed ones (Is != I), and I = 384 (three gate_up weight tiles).
+@pytest.mark.parametrize("shape,T,zipf", [(MoEShape(1024, 128, 8, 256, 0), 2048, True),
+                                          (MoEShape(512, 16, 2, 256, 128), 1500, False),
+                                          (MoEShape(768, 64, 4, 384, 256), 1000, True)])
+def test_block_prefill_packed_weights(gpu, shape, T, zipf):
+    bias = None
+    if zipf:
+        bias = zipf_bias(torch.Generator().manual_seed(shape.num_experts), shape.num_experts)
+    _run_and_check(shape, T, gpu, seed=T + 1, bias=bias, sample=96, pack=True)
+    w, g = make_layer(shape, seed=T, device="cpu")
+    x = make_x(g, T, shape.hidden_size, device="cpu").to(gpu)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    if bias is not None:
+        blk.gate.logit_bias = bias.to(gpu)
+    y0 = blk(x)
+    blk.pack_tiled_()
+    assert blk.layer().gate_up_tiled and blk.layer().down_tiled
+    y1 = blk(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
 
 
 def test_block_prefill_tiled_shared(gpu):
