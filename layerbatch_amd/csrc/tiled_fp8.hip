@@ -110,8 +110,10 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   // Ring copies, as in the bf16 kernels: wave copy i fills one 1 KB LDS block of kRowsPerLoad
   // rows; lane l fetches the chunk that the swizzle places at slot l.
   const int lrow = lane / kChunks, lpos = lane % kChunks;
-  // Copy addresses as a wave-uniform base plus a 32-bit lane offset (one VGPR per copy): the
-  // kRowsPerLoad rows of one copy are consecutive rows of one weight matrix.
+  // Copies through buffer resources, as in the bf16 kernels (there, global_load_lds made the
+  // compiler wait for every outstanding LDS read before each MFMA step): a wave-uniform
+  // descriptor per copy, a 32-bit lane offset (one VGPR per copy), the k-tile's byte step in
+  // the scalar offset. The kRowsPerLoad rows of one copy are consecutive rows of one matrix.
   const uint8_t* abase[kALoads];
   uint32_t aoff[kALoads];
 #pragma unroll
@@ -150,9 +152,11 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     constexpr int nb = kWT / 64;
     const int pos = (w % nb) * 64 + lane;
     const int lt = (pos / (16 * kN16)) * (16 * kN16) + 16 * (pos % kN16) + (pos % (16 * kN16)) / kN16;
-    const float* sp = src_sc + static_cast<int64_t>(src_row(lt)) * (src_ld / 128);
+    const __amdgpu_buffer_rsrc_t srs = raw_rsrc(src_sc);
+    const uint32_t soff = static_cast<uint32_t>(src_row(lt)) * static_cast<uint32_t>(src_ld / 128) * 4;
     for (int kb = w / nb; kb < nk; kb += kWaves / nb)
-      __builtin_amdgcn_global_load_lds(sp + kb, (lds_ptr)(scl + kb * kWT + (w % nb) * 64), 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_ptr)(scl + kb * kWT + (w % nb) * 64), 4,
+                                               soff, kb * 4, 0, 0);
     if (w == 0) {
       const float* wsp = lane < nk ? sw0 + lane : (lane < 2 * nk ? sw1 + (lane - nk) : sw0);
       __builtin_amdgcn_global_load_lds(wsp, (lds_ptr)(scl + kActScales), 4, 0, 0);
@@ -168,18 +172,22 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
 
   // narrow and tiny tiles' weight copies are non-temporal, as in the bf16 kernel
   constexpr int kWeightPolicy = S::kWT < kWM ? 2 : 0;
+  __amdgpu_buffer_rsrc_t ars[kALoads];
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) ars[i] = raw_rsrc(abase[i]);
+  const __amdgpu_buffer_rsrc_t brs = raw_rsrc(src);
   auto issue = [&](int stage, int k0) {
     u32x4* buf = lds + stage * kStageU4;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
-      __builtin_amdgcn_global_load_lds(abase[i] + (aoff[i] + static_cast<uint32_t>(k0)),
-                                       (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks),
-                                       16, 0, kWeightPolicy);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ars[i], (lds_ptr)(buf + (w * kALoads + i) * kRowsPerLoad * kChunks), 16, aoff[i], k0,
+          0, kWeightPolicy);
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i)
-      __builtin_amdgcn_global_load_lds(src + (boff[i] + static_cast<uint32_t>(k0)),
-                                       (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks),
-                                       16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          brs, (lds_ptr)(buf + (kWM + (w * kBLoads + i) * kRowsPerLoad) * kChunks), 16, boff[i],
+          k0, 0, 0);
   };
 
   const int r16 = lane & 15, q = lane >> 4;
