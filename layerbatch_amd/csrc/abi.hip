@@ -218,9 +218,23 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
                                    max_tiles, tiles, s));
     tiles_built = true;
   } else if (!permuted && !perm_in_gate_up) {
-    LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
-                             at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
-                             at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
+    const bool tiled = use_tiled(gw, T, k) &&
+                       (!is_fp8(L) || tiled_fp8_supported(gw, T, T * k + (with_shared ? T : 0)));
+    if (tiled && perm_chunked(T * k, E)) {
+      // prefill GEMMs: the permutation's scatter and the tile list in one launch
+      int32_t* base = at<int32_t>(ws, w, R_BASE);
+      int32_t* lrank = at<int32_t>(ws, w, R_LRANK);
+      LBMOE_TRY(launch_perm_count_scan(idx, idx_bytes, T, k, E, at<int32_t>(ws, w, R_HIST), base,
+                                       lrank, counts, s));
+      LBMOE_TRY(launch_perm_scatter_build(idx, idx_bytes, T, k, base, counts, lrank, offsets,
+                                          perm_tok, at<int32_t>(ws, w, R_PERM_SLOT), inv, gw,
+                                          with_shared, max_tiles, tiles, s));
+      tiles_built = true;
+    } else {
+      LBMOE_TRY(launch_permute(idx, idx_bytes, T, k, E, with_shared, counts, offsets, perm_tok,
+                               at<int32_t>(ws, w, R_PERM_SLOT), inv, at<int32_t>(ws, w, R_HIST),
+                               at<int32_t>(ws, w, R_BASE), at<int32_t>(ws, w, R_LRANK), s));
+    }
   }
   LBMOE_TRY(ev->mark(s));
   void* act = at<void>(ws, w, R_ACT);

@@ -154,4 +154,12 @@ __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
+
+// Expert id i of a routing table of int32 (IB = 4) or int64 (IB = 8) entries.
+template <int IB>
+__device__ __forceinline__ int load_expert(const void* idx, int64_t i) {
+  if constexpr (IB == 8) return static_cast<int>(reinterpret_cast<const int64_t*>(idx)[i]);
+  else return reinterpret_cast<const int32_t*>(idx)[i];
+}
+
 }  // namespace lbmoe

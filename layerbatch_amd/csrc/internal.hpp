@@ -258,6 +258,19 @@ hipError_t launch_router_route(const void* x, const void* wg, const float* bias,
                                hipStream_t s);
 hipError_t launch_perm_scan(const int32_t* hist, int nchunks, int E, int32_t* base,
                             int32_t* totals, hipStream_t s);
+// The chunked permutation of launch_permute as two steps, for the prefill GEMMs: the count
+// and scan passes (perm_count, perm_expert_scan: hist, base, lrank, counts), then the scatter
+// with the GEMMs' tile list in one launch. perm_chunked: whether launch_permute would chunk a
+// batch of V entries (otherwise it permutes in one workgroup).
+bool perm_chunked(int64_t V, int E);
+hipError_t launch_perm_count_scan(const void* idx, int idx_bytes, int64_t T, int k, int E,
+                                  int32_t* hist, int32_t* base, int32_t* lrank, int32_t* counts,
+                                  hipStream_t s);
+hipError_t launch_perm_scatter_build(const void* idx, int idx_bytes, int64_t T, int k,
+                                     const int32_t* base, const int32_t* counts,
+                                     const int32_t* lrank, int32_t* offsets, int32_t* perm_tok,
+                                     int32_t* perm_slot, int32_t* inv, const GroupWeights& gw,
+                                     bool shared, int max_tiles, int32_t* tiles, hipStream_t s);
 hipError_t launch_scatter_build(const int32_t* idx, int64_t T, int k, const int32_t* base,
                                 const int32_t* counts, const int32_t* lrank, int32_t* offsets,
                                 int32_t* perm_tok, int32_t* perm_slot, int32_t* inv,

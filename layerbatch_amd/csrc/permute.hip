@@ -22,12 +22,6 @@
 
 namespace lbmoe {
 
-template <int IB>
-__device__ __forceinline__ int load_expert(const void* idx, int64_t i) {
-  if constexpr (IB == 8) return static_cast<int>(reinterpret_cast<const int64_t*>(idx)[i]);
-  else return reinterpret_cast<const int32_t*>(idx)[i];
-}
-
 // Ranks one chunk's entries. Returns per-lane (expert, rank) for round r in e_out/rk_out.
 // All expert ids of the chunk are loaded before the ranking so the loads overlap.
 template <int IB, int ROUNDS>
@@ -331,6 +325,23 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
   perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
   perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, counts,
                                        offsets, lrank, perm_tok, perm_slot, inv);
+  return hipGetLastError();
+}
+
+bool perm_chunked(int64_t V, int E) {
+  return V > 2 * kPermSingle && !(V <= 4 * kPermSingle && E <= 512);
+}
+
+hipError_t launch_perm_count_scan(const void* idx, int idx_bytes, int64_t T, int k, int E,
+                                  int32_t* hist, int32_t* base, int32_t* lrank, int32_t* counts,
+                                  hipStream_t s) {
+  const int V = static_cast<int>(T * k), nbits = bits_for(E);
+  const int nblk = static_cast<int>(perm_blocks(V));
+  if (idx_bytes == 8)
+    perm_count<8><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist, lrank);
+  else
+    perm_count<4><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist, lrank);
+  perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
   return hipGetLastError();
 }
 

@@ -318,6 +318,55 @@ __global__ __launch_bounds__(1024) void scatter_build_kernel(
   inv[ts] = pos;
 }
 
+// The same for the chunks of launch_permute's count pass (perm_count): chunk c holds entries
+// v = c * kPermChunk + r * 64 + lane (v = s * T + t, the reference's (slot, token) order) with
+// their ranks in lrank. Scatter workgroup c places chunk c, wave r its round r (with
+// 16 chunks per workgroup, as above, a prefill batch's few hundred chunks ran on a dozen CUs
+// and the launch took longer than the scatter and tile build it replaced); ids outside [0, E)
+// get inv = -1.
+template <int IB>
+__global__ __launch_bounds__(1024) void perm_scatter_build_kernel(
+    const void* idx, int T, int k, int V, int nblk, const int32_t* __restrict__ base,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ lrank,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tok, int32_t* __restrict__ perm_slot,
+    int32_t* __restrict__ inv, int n_scatter, int E, int shared, int sh_row0, int max_tiles,
+    int wide, int narrow, int tiny, int I, int Is, int H, int grid_gu, int grid_dn,
+    int32_t* __restrict__ tiles) {
+  // the tile-list workgroups first, so that their work overlaps the scatter's
+  const int n_build = static_cast<int>(gridDim.x) - n_scatter;
+  if (static_cast<int>(blockIdx.x) < n_build) {
+    build_tiles_body(counts, nullptr, E, shared, T, sh_row0, max_tiles, wide, narrow, tiny, I, Is,
+                     H, grid_gu, grid_dn, tiles, blockIdx.x, n_build);
+    return;
+  }
+  __shared__ int wsum[16];
+  __shared__ int s_off[1024];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int c = static_cast<int>(blockIdx.x) - n_build;
+  int ex;
+  const int total = block_scan_1024(tid < E ? counts[tid] : 0, ex, wsum);
+  if (tid < E) s_off[tid] = ex;
+  if (c == 0) {
+    if (tid < E) offsets[tid] = ex;
+    if (tid == 0) offsets[E] = total;
+  }
+  __syncthreads();
+  if (wave >= kPermChunk / kWave) return;
+  const int v = c * kPermChunk + wave * kWave + lane;
+  if (v >= V) return;
+  const int s = v / T, t = v - s * T;
+  const int64_t ts = static_cast<int64_t>(t) * k + s;
+  const int e = load_expert<IB>(idx, ts);
+  if (e < 0 || e >= E) {
+    inv[ts] = -1;
+    return;
+  }
+  const int pos = s_off[e] + base[static_cast<int64_t>(e) * nblk + c] + lrank[v];
+  perm_tok[pos] = t;
+  perm_slot[pos] = s;
+  inv[ts] = pos;
+}
+
 // ---- one token tile --------------------------------------------------------------------------
 // MODE kDown: out[row, h] = act[row] . Wd_g[h];  kGateUp: act[row, c] = silu(gate) * up;
 // kRouter: logits[t, e] = x[t] . Wg[e] (gw.gate_up holds the router weight, gw.E its rows).
@@ -1150,6 +1199,27 @@ hipError_t launch_scatter_build(const int32_t* idx, int64_t T, int k, const int3
       idx, static_cast<int>(T), k, nb, base, counts, lrank, offsets, perm_tok, perm_slot, inv,
       n_scatter, gw.E, shared ? 1 : 0, gw.sh_row0, max_tiles, Wide::kWT, Narrow::kWT, Tiny::kWT,
       gw.I, gw.Is, gw.H, grid_gu, grid_dn, tiles);
+  return hipGetLastError();
+}
+
+hipError_t launch_perm_scatter_build(const void* idx, int idx_bytes, int64_t T, int k,
+                                     const int32_t* base, const int32_t* counts,
+                                     const int32_t* lrank, int32_t* offsets, int32_t* perm_tok,
+                                     int32_t* perm_slot, int32_t* inv, const GroupWeights& gw,
+                                     bool shared, int max_tiles, int32_t* tiles, hipStream_t s) {
+  const int V = static_cast<int>(T * k);
+  const int nblk = static_cast<int>(perm_blocks(V));
+  const int n_scatter = nblk;
+  const int grid_gu = tiled_grid(gw, max_tiles, true), grid_dn = tiled_grid(gw, max_tiles, false);
+  const int blocks = build_blocks(max_tiles, grid_gu + grid_dn);
+#define LBMOE_PSB(IB)                                                                           \
+  perm_scatter_build_kernel<IB><<<n_scatter + blocks, 1024, 0, s>>>(                           \
+      idx, static_cast<int>(T), k, V, nblk, base, counts, lrank, offsets, perm_tok, perm_slot, \
+      inv, n_scatter, gw.E, shared ? 1 : 0, gw.sh_row0, max_tiles, Wide::kWT, Narrow::kWT,     \
+      Tiny::kWT, gw.I, gw.Is, gw.H, grid_gu, grid_dn, tiles)
+  if (idx_bytes == 8) LBMOE_PSB(8);
+  else LBMOE_PSB(4);
+#undef LBMOE_PSB
   return hipGetLastError();
 }
 
