@@ -576,16 +576,30 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   // interleaved with the last k-step's MFMAs, so neither the copy issue nor the LDS read
   // latency of the next k-tile stands between two MFMAs.
   const int nk = K / kBK;
-  if constexpr (S::kAsym) {
-#pragma unroll
-    for (int st = 0; st < kStages; ++st) {
-      if (st < nk) issue_a(st, st);
-      if (st < S::kBStages && st < nk) issue_b(st, st);
-    }
+  // Wide expert tiles (MFMA-bound) put only stage 0 out before the first wait. A wave reaches
+  // its wait once it has issued every copy before it, and the CU's copy path takes the waves'
+  // copies in turn: with the whole ring issued up front, the second wave of each SIMD saw its
+  // stage 0 land only after the path had drained the entire fill (160 KB; 1.9 instead of
+  // 1.2 us). Their other stages follow in k-tile 0 (fill_stage), in the same order as up
+  // front, so every later wait counts the same younger copies. Narrow and tiny tiles are
+  // bound by HBM and keep the whole fill up front: stages issued later cost them more than the
+  // earlier start gains (E=512 T=4096 down 240 -> 243 us). There a barrier after stage 0 puts
+  // every wave's stage 0 on the copy path before any wave's later stages.
+  constexpr bool kLazyFill = !ROUTER && S::kWT == kWM;
+  // Stage st's copies of the fill, in the order of the asymmetric ring (A0 B0 A1 B1 A2) or the
+  // symmetric one (A0 B0 A1 B1 A2 B2 ...). CHECK: nk may be at most st.
+  auto fill_stage = [&]<bool CHECK>(int st) {
+    if (!CHECK || st < nk) issue_a(st, st);
+    if (st < S::kBStages && (!CHECK || st < nk)) issue_b(st, st);
+  };
+  if constexpr (kLazyFill) {
+    issue(0, 0);
   } else {
 #pragma unroll
-    for (int st = 0; st < kStages; ++st)
-      if (st < nk) issue(st, st);
+    for (int st = 0; st < kStages; ++st) {
+      fill_stage.template operator()<true>(st);
+      if (st == 0) ring_barrier();
+    }
   }
   const int mr = lane & 31, mk = lane >> 5;   // MFMA operand: row l%32, k-chunk half l/32
   auto read_frags = [&](int kt, int ks, u32x4 (&fa)[kMT], u32x4 (&fb)[kNT]) {
@@ -621,16 +635,31 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   u32x4 fa[2][kMT], fb[2][kNT];
   // One k-tile. NEXT: a k-tile follows (wait, barrier, read its first fragments); REFILL: the
   // freed buffers take k-tile kt + kStages (2: both operands; 1: the asymmetric ring's token
-  // operand only, whose ring runs one k-tile shorter). Specialised at compile time so that the loop body
-  // has no branches around the MFMAs.
+  // operand only, whose ring runs one k-tile shorter). FILL (k-tile 0 when nk > kStages): the
+  // ring's stages 1 .. kStages - 1 go out behind the MFMAs of the first k-steps, one stage per
+  // k-step. Specialised at compile time so that the loop body has no branches around the MFMAs.
+  static_assert(kStages <= kKSteps, "the fill issues one stage per k-step of k-tile 0");
   int claim = -1;      // PERSIST: home-queue slot claimed for the next item (-1: none)
-  auto ktile = [&]<bool NEXT, int REFILL, bool CLAIM = false>(int kt) {
+  auto ktile = [&]<bool NEXT, int REFILL, bool CLAIM = false, bool FILL = false>(int kt) {
 #pragma unroll
     for (int ks = 0; ks + 1 < kKSteps; ++ks) {
       read_frags(kt, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       mfma_all(fa[ks & 1], fb[ks & 1]);
-      sched_reads();
-      if constexpr (kMfmas > kPaired) __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPaired, 0);
+      constexpr int kRest = kMfmas - kPaired;
+      if (FILL && ks + 1 < kStages) {
+        fill_stage.template operator()<false>(ks + 1);
+        sched_reads();
+        constexpr int kPer = (kLoads + (kRest > 0 ? kRest : 1) - 1) / (kRest > 0 ? kRest : 1);
+#pragma unroll
+        for (int r = 0; r < kRest; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, kPer, 0);
+        }
+        if constexpr (kRest == 0) __builtin_amdgcn_sched_group_barrier(0x020, kLoads, 0);
+      } else {
+        sched_reads();
+        if constexpr (kRest > 0) __builtin_amdgcn_sched_group_barrier(0x008, kRest, 0);
+      }
     }
     constexpr int kl = (kKSteps - 1) & 1;
     if constexpr (NEXT) {
@@ -679,7 +708,9 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
       }
     }
   };
-  if constexpr (S::kAsym) {
+  if constexpr (kLazyFill) {
+    wait_vmcnt<0>();                   // stage 0, the only copies out
+  } else if constexpr (S::kAsym) {
     // k-tile 0 must have landed; younger: k-tile 1 (both operands) and k-tile 2's weights
     if (nk > 2) wait_vmcnt<kLoads + kALoads>();
     else if (nk > 1) wait_vmcnt<kLoads>();
@@ -690,6 +721,14 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   ring_barrier();
   read_frags(0, 0, fa[0], fb[0]);
   int kt = 0;
+  if constexpr (kLazyFill) {
+    if (nk > kStages) {
+      ktile.template operator()<true, 2, false, true>(kt++);
+    } else {
+#pragma unroll
+      for (int st = 1; st < kStages; ++st) fill_stage.template operator()<true>(st);
+    }
+  }
   for (; kt + kStages < nk; ++kt) ktile.template operator()<true, 2>(kt);
   if constexpr (S::kAsym)
     for (; kt + S::kBStages < nk; ++kt) ktile.template operator()<true, 1>(kt);
