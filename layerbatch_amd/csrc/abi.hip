@@ -41,9 +41,11 @@ WsLayout ws_layout(const lbmoe_layer& L, int64_t T) {
                                       L.shared_intermediate_size, H);
   if (is_fp8(L)) {
     w.bytes[R_XQ] = T * H;
-    w.bytes[R_XS] = T * (H / 128) * 4;
+    // the scale regions end in 16 spare bytes: the tiled fp8 GEMMs copy a row's scales in
+    // 16-byte pieces, whose last may reach 12 bytes past the final row
+    w.bytes[R_XS] = T * (H / 128) * 4 + 16;
     w.bytes[R_ACTQ] = Vs * Imax;
-    w.bytes[R_ACTS] = Vs * (Imax / 128) * 4;
+    w.bytes[R_ACTS] = Vs * (Imax / 128) * 4 + 16;
   }
   size_t off = 0;
   for (int r = 0; r < R_COUNT_; ++r) {

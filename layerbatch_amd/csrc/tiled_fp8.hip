@@ -144,19 +144,21 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   }
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  // Scale copies (4 bytes per lane). Activation scales: scl[kb * kWT + pos], pos =
-  // wn' * 16 kN16 + r * kN16 + t for local token wn' * 16 kN16 + 16 t + r, so that a lane
-  // reads its kN16 columns' scales of one k-tile with one load. Wave w copies 64-entry block
-  // w % nb of k-tiles w / nb, w / nb + 8 / nb, ...; wave 0 also copies the weight-scale rows.
+  // Scale copies. Activation scales: token lt's row of nk scales goes to LDS as nc = ceil(nk/4)
+  // 16-byte pieces, scl[lt * 4 nc + kb], a wave copy moving 64 pieces (64 / nc tokens' rows).
+  // Copied as one 4-byte scale per lane (64 token rows per copy, each its own cache line) these
+  // took 4x the copies and ~64 texture-address cycles apiece, ~4k cycles of every item's fill
+  // at K = 2048. A row's last piece may reach 12 bytes past its nk scales (into the next row,
+  // or the scale region's 16-byte tail). Wave 0 also copies the weight-scale rows.
   {
-    constexpr int nb = kWT / 64;
-    const int pos = (w % nb) * 64 + lane;
-    const int lt = (pos / (16 * kN16)) * (16 * kN16) + 16 * (pos % kN16) + (pos % (16 * kN16)) / kN16;
+    const int nc = (nk + 3) / 4;
     const __amdgpu_buffer_rsrc_t srs = raw_rsrc(src_sc);
-    const uint32_t soff = static_cast<uint32_t>(src_row(lt)) * static_cast<uint32_t>(src_ld / 128) * 4;
-    for (int kb = w / nb; kb < nk; kb += kWaves / nb)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_ptr)(scl + kb * kWT + (w % nb) * 64), 4,
-                                               soff, kb * 4, 0, 0);
+    const uint32_t row_bytes = static_cast<uint32_t>(src_ld / 128) * 4;
+    for (int c0 = w * 64; c0 < kWT * nc; c0 += kThreads) {
+      const int c = c0 + lane, lt = c / nc;
+      const uint32_t off = static_cast<uint32_t>(src_row(lt)) * row_bytes + (c - lt * nc) * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_ptr)(scl + c0 * 4), 16, off, 0, 0, 0);
+    }
     if (w == 0) {
       const float* wsp = lane < nk ? sw0 + lane : (lane < 2 * nk ? sw1 + (lane - nk) : sw0);
       __builtin_amdgcn_global_load_lds(wsp, (lds_ptr)(scl + kActScales), 4, 0, 0);
@@ -222,10 +224,11 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   // Scales of k-tile kt: sc[h][t] = weight scale h * activation scale of column t, h = 0 for
   // gate and down tiles, 1 for up tiles. The next k-tile's are read halfway through a k-tile.
   float sa[kN16], w0, w1;
+  const int scl_ld = 4 * ((nk + 3) / 4);          // activation scales per token in LDS
   auto read_scales = [&](int kt) {
-    const float* a = scl + kt * kWT + wn * (16 * kN16) + r16 * kN16;
+    const float* a = scl + (wn * (16 * kN16) + r16) * scl_ld + kt;
 #pragma unroll
-    for (int t = 0; t < kN16; ++t) sa[t] = a[t];
+    for (int t = 0; t < kN16; ++t) sa[t] = a[16 * t * scl_ld];
     w0 = wsc[(GATEUP ? 0 : wm * kRW / 128) * nk + kt];
     w1 = GATEUP ? wsc[nk + kt] : w0;
   };
