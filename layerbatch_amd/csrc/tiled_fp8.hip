@@ -205,9 +205,13 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   // once the last A tile's fragments are in registers, each wave waits for its copies of
   // stage kt+1 and meets the others at the barrier, then reads stage kt+1's B fragments and
   // first A fragment and refills stage kt's buffer, interleaved with the last MFMAs.
+  // a barrier after stage 0 puts every wave's stage 0 on the CU's copy path before any wave's
+  // later stages (a wave reaches its wait only once it has issued all of its copies)
 #pragma unroll
-  for (int st = 0; st < kStages; ++st)
+  for (int st = 0; st < kStages; ++st) {
     if (st < nk) issue(st, st * 128);
+    if (st == 0) ring_barrier();
+  }
   wait_ring<kStages - 1, kLoads>(nk - 1);
   ring_barrier();
 
