@@ -192,7 +192,7 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
                            const WsLayout& w, bool with_shared, hipStream_t s,
                            StageEvents* ev = nullptr, bool permuted = false,
                            const SmallRoute* rt = nullptr, bool own_ids = false,
-                           bool chunked = false) {
+                           bool chunked = false, bool x_quantised = false) {
   StageEvents none{nullptr, 0, 0};
   if (!ev) ev = &none;
   const int k = L.top_k, E = L.num_experts, H = L.hidden_size;
@@ -248,7 +248,7 @@ static int32_t run_experts(const lbmoe_layer& L, const void* x, const void* idx,
     void* actq = at<void>(ws, w, R_ACTQ);
     float* acts = at<float>(ws, w, R_ACTS);
     const int64_t rows = T * k + (with_shared ? T : 0);
-    LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
+    if (!x_quantised) LBMOE_TRY(launch_quant_groups_fp8(x, T, H, H, xq, xs, s));
     if (use_tiled(gw, T, k) && tiled_fp8_supported(gw, T, rows)) {
       if (!tiles_built)
         LBMOE_TRY(launch_build_tiles(counts, offsets, gw, with_shared, T, max_tiles, tiles, s));
@@ -480,10 +480,16 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
     LBMOE_TRY(ev->mark(s));
     return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, true);
   }
+  // fp8 layers with a shared expert: the selection kernel, which reads x for the shared gate,
+  // also writes x's e4m3 codes and scales
+  const bool fuse_q = is_fp8(L) && sh;
   LBMOE_TRY(launch_route_topk(logits, L.logit_bias, x, L.shared_expert_gate, T, L.num_experts,
-                              L.hidden_size, L.top_k, idx, 4, topw, sgate, s));
+                              L.hidden_size, L.top_k, idx, 4, topw, sgate, s,
+                              fuse_q ? at<void>(ws, w, R_XQ) : nullptr,
+                              fuse_q ? at<float>(ws, w, R_XS) : nullptr));
   LBMOE_TRY(ev->mark(s));
-  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, false, nullptr, true);
+  return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, false, nullptr, true,
+                     false, fuse_q);
 }
 
 }  // namespace lbmoe

@@ -131,9 +131,12 @@ hipError_t launch_router_logits(const void* x, const void* wg, int64_t T, int E,
 hipError_t launch_add_rmsnorm_router(const void* hidden, const void* residual, const void* norm_w,
                                      float eps, const void* wg, int64_t T, int E, int H,
                                      void* logits, void* x_out, void* res_out, hipStream_t s);
+// xq, xs (fp8 layers, with sgate): x's e4m3 codes and group scales, written with the shared
+// gate's loads of x (quant_groups_kernel's layout), so the layer needs no separate pass.
 hipError_t launch_route_topk(const void* logits, const float* bias, const void* x,
                              const void* w_sg, int64_t T, int E, int H, int k, void* idx,
-                             int idx_bytes, void* topw, float* sgate, hipStream_t s);
+                             int idx_bytes, void* topw, float* sgate, hipStream_t s,
+                             void* xq = nullptr, float* xs = nullptr);
 bool route_perm_small_supported(int64_t T, int k, int E);
 hipError_t launch_route_perm_small(const void* logits, const float* bias, const void* x,
                                    const void* w_sg, int64_t T, int E, int H, int k, int32_t* idx,

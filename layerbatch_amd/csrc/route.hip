@@ -31,15 +31,18 @@ __global__ __launch_bounds__(256) void route_topk(const uint16_t* __restrict__ l
                                                   const uint16_t* __restrict__ w_sg, int T,
                                                   int E, int H, int k, void* idx_out,
                                                   int idx_bytes, uint16_t* __restrict__ topw,
-                                                  float* __restrict__ sgate) {
+                                                  float* __restrict__ sgate,
+                                                  uint8_t* __restrict__ xq,
+                                                  float* __restrict__ xs) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  route_token<EPL>(logits, bias, x, w_sg, t, E, H, k, idx_out, idx_bytes, topw, sgate);
+  route_token<EPL>(logits, bias, x, w_sg, t, E, H, k, idx_out, idx_bytes, topw, sgate, xq, xs);
 }
 
 hipError_t launch_route_topk(const void* logits, const float* bias, const void* x,
                              const void* w_sg, int64_t T, int E, int H, int k, void* idx,
-                             int idx_bytes, void* topw, float* sgate, hipStream_t s) {
+                             int idx_bytes, void* topw, float* sgate, hipStream_t s, void* xq,
+                             float* xs) {
   const dim3 grid(static_cast<unsigned>((T + 3) / 4));
   const auto* lg = static_cast<const uint16_t*>(logits);
   const auto* xx = static_cast<const uint16_t*>(x);
@@ -47,7 +50,8 @@ hipError_t launch_route_topk(const void* logits, const float* bias, const void* 
   auto* tw = static_cast<uint16_t*>(topw);
   const int Ti = static_cast<int>(T);
 #define LBMOE_ROUTE(EPL)                                                                       \
-  route_topk<EPL><<<grid, 256, 0, s>>>(lg, bias, xx, ws, Ti, E, H, k, idx, idx_bytes, tw, sgate)
+  route_topk<EPL><<<grid, 256, 0, s>>>(lg, bias, xx, ws, Ti, E, H, k, idx, idx_bytes, tw, sgate, \
+                                       static_cast<uint8_t*>(xq), xs)
   if (E <= 64) LBMOE_ROUTE(1);
   else if (E <= 128) LBMOE_ROUTE(2);
   else if (E <= 256) LBMOE_ROUTE(4);

@@ -198,16 +198,28 @@ __device__ __forceinline__ void route_select8(const float (&z)[EPG], int E, int 
   }
 }
 
-// sgate[t] = sigmoid(bf16(x[t] . w_sg)), every lane of the wave calling it.
+// sgate[t] = sigmoid(bf16(x[t] . w_sg)), every lane of the wave calling it. With xq (fp8
+// layers): the row's e4m3 codes and per-128-channel scales as well, as quant_groups_kernel
+// writes them (xq[t, :], xs[t, H / 128]). A load of the loop covers channels 8 lane + 512 i, so
+// the 16 lanes of a DPP row hold exactly one 128-channel group: the row is quantised from the
+// registers the dot product reads, and its separate pass over x is saved.
 __device__ __forceinline__ void shared_gate(const uint16_t* __restrict__ x,
                                             const uint16_t* __restrict__ w_sg, int t, int H,
-                                            float* __restrict__ sgate) {
+                                            float* __restrict__ sgate,
+                                            uint8_t* __restrict__ xq = nullptr,
+                                            float* __restrict__ xs = nullptr) {
   const int lane = lane_id();
   const uint16_t* xr = x + static_cast<int64_t>(t) * H;
   float d = 0.f;
   for (int c = lane * 8; c < H; c += kWave * 8) {
     const u32x4 a = ld16(xr + c);
     const u32x4 b = ld16(w_sg + c);
+    if (xq != nullptr) {                 // whole DPP rows are active: H is a multiple of 128
+      float sc;
+      const u32x2 q = quant_group16(a, sc);
+      *reinterpret_cast<u32x2*>(xq + static_cast<int64_t>(t) * H + c) = q;
+      if ((lane & 15) == 0) xs[static_cast<int64_t>(t) * (H / 128) + c / 128] = sc;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       d += bf_lo(a[q]) * bf_lo(b[q]);
@@ -227,7 +239,9 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
                                             const uint16_t* __restrict__ w_sg, int t, int E,
                                             int H, int k, void* idx_out, int idx_bytes,
                                             uint16_t* __restrict__ topw,
-                                            float* __restrict__ sgate) {
+                                            float* __restrict__ sgate,
+                                            uint8_t* __restrict__ xq = nullptr,
+                                            float* __restrict__ xs = nullptr) {
   const int lane = lane_id();
   const uint16_t* lrow = logits + static_cast<int64_t>(t) * E;
   // unconditional loads (lanes past E read expert E-1 and are masked): a load under a
@@ -248,7 +262,7 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
     z[j] = (!(v == v) || e >= E) ? -INFINITY : v;      // a NaN logit is never preferred
   }
   // the shared-expert gate, its loads in flight together with the logits'
-  if (sgate != nullptr) shared_gate(x, w_sg, t, H, sgate);
+  if (sgate != nullptr) shared_gate(x, w_sg, t, H, sgate, xq, xs);
   route_select<EPL>(z, E, k, static_cast<int64_t>(t) * k, idx_out, idx_bytes, topw, nullptr);
 }
 
