@@ -98,10 +98,27 @@ __device__ __forceinline__ u32x2 quant_group16(u32x4 v, float& s) {
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
   amax = row16_max(amax);
   s = fp8_scale_of(amax);
+  // x / s rounded as the division rounds it, with one division per group instead of per value
+  // (Markstein): y = RN(1/s); q = RN(x y) is within an ulp of x / s, r = fma(-q, s, x) is exact
+  // and RN(q + r y) = RN(x / s) while nothing underflows. Quotients under 2^-12, where r may
+  // underflow, still land below e4m3's smallest step, so the codes agree; the sign is taken
+  // from x (the sequence turns -0 into +0). Checked against the division on 5e8 bf16 values
+  // and adversarial pairs (float32, fma, no contraction). Groups with s < 2^-80 divide.
+  float q[8];
+  if (s >= 0x1p-80f) {
+    const float y = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float q0 = x[j] * y;
+      q[j] = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, s, x[j]), y, q0), x[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = x[j] / s;
+  }
   u32x2 c;
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-    c[h] = e4m3x4(x[4 * h] / s, x[4 * h + 1] / s, x[4 * h + 2] / s, x[4 * h + 3] / s);
+  for (int h = 0; h < 2; ++h) c[h] = e4m3x4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
   return c;
 }
 
