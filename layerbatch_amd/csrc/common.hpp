@@ -103,9 +103,11 @@ __device__ __forceinline__ u32x2 quant_group16(u32x4 v, float& s) {
   // and RN(q + r y) = RN(x / s) while nothing underflows. Quotients under 2^-12, where r may
   // underflow, still land below e4m3's smallest step, so the codes agree; the sign is taken
   // from x (the sequence turns -0 into +0). Checked against the division on 5e8 bf16 values
-  // and adversarial pairs (float32, fma, no contraction). Groups with s < 2^-80 divide.
+  // and adversarial pairs (float32, fma, no contraction). Groups with s < 2^-80 divide, and
+  // so do groups with s > 2^100 (an infinite value makes s infinite and y zero, where r would
+  // be 0 * inf).
   float q[8];
-  if (s >= 0x1p-80f) {
+  if (s >= 0x1p-80f && s <= 0x1p+100f) {
     const float y = 1.0f / s;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {

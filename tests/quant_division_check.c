@@ -4,7 +4,8 @@
 // x / s bit for bit wherever |x / s| >= 2^-12, and below that lies under e4m3's smallest step
 // (2^-10) with x / s's sign, so the e4m3 codes agree everywhere. Inputs: 128-value groups of
 // bf16 values (Gaussian, magnitudes 2^-40 .. 2^19, signed zeros) with s = amax / 448, and
-// random (x, s) pairs with |x| <= 448 s; groups with s < 2^-80 are skipped (they divide).
+// random (x, s) pairs with |x| <= 448 s; groups with s outside [2^-80, 2^100] are skipped (they
+// divide).
 // Usage: quant_division_check [groups]; exit status 1 on any mismatch.
 #include <stdio.h>
 #include <stdint.h>
@@ -27,7 +28,7 @@ int main(int argc, char** argv) {
       x[i] = v; float a = fabsf(v); if (a > amax) amax = a;
     }
     float s = amax > 0.f ? amax / 448.0f : 1.0f;
-    if (s < 0x1p-80f) continue;
+    if (s < 0x1p-80f || s > 0x1p+100f) continue;
     float y = 1.0f / s;
     for (int i = 0; i < 128; ++i) {
       float q = x[i] * y;
@@ -45,7 +46,7 @@ int main(int argc, char** argv) {
     uint32_t ub = 0x3f800000u | (uint32_t)(rnd() & 0x7fffff), ux = (uint32_t)(rnd() & 0xffff0000u);
     float s, xv; memcpy(&s, &ub, 4); memcpy(&xv, &ux, 4);
     s = ldexpf(s, (int)(rnd() % 100) - 60);
-    if (!(fabsf(xv) <= 448.0f * s) || s < 0x1p-80f) continue;
+    if (!(fabsf(xv) <= 448.0f * s) || s < 0x1p-80f || s > 0x1p+100f) continue;
     float y = 1.0f / s, q = xv * y, r = fmaf(-q, s, xv), q2 = copysignf(fmaf(r, y, q), xv), ref = xv / s;
     uint32_t a, b; memcpy(&a, &q2, 4); memcpy(&b, &ref, 4); ++checked;
     const int mis = fabsf(ref) >= 0x1p-12f ? a != b : (!(fabsf(q2) < 0x1p-10f) || signbit(q2) != signbit(ref));
