@@ -134,6 +134,18 @@ def settle(call, warmup, settle_s):
         torch.cuda.synchronize()
 
 
+def check_all(rcs, what="lbmoe_forward"):
+    """Status of every timed call, checked once the timed region has ended: a failed call
+    invalidates the measurement."""
+    from layerbatch_amd import _lib
+    for rc in rcs:
+        _lib.check(rc, what)
+
+
+# Timed calls of every prefill-sized measurement, whatever --steps is (one call is ~1 ms).
+MIN_PREFILL_STEPS = 10
+
+
 def measure(blk, x, steps, warmup, hip, settle_s=0.0):
     """Wall time per call over `steps` plain calls, then per-stage HIP-event times over
     `steps` profiled calls. Returns a dict of timings and routing statistics."""
@@ -148,10 +160,10 @@ def measure(blk, x, steps, warmup, hip, settle_s=0.0):
     args = (ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws), ws.numel(), stream)
     settle(lambda: _lib.check(lib.lbmoe_forward(*args), "lbmoe_forward"), warmup, settle_s)
     t0 = time.perf_counter()
-    for _ in range(steps):
-        lib.lbmoe_forward(*args)
+    rcs = [lib.lbmoe_forward(*args) for _ in range(steps)]
     torch.cuda.synchronize()
     wall_us = (time.perf_counter() - t0) / steps * 1e6
+    check_all(rcs)
 
     n_ev = _lib.LBMOE_PROFILE_EVENTS
     evsets = [hip.create(n_ev) for _ in range(steps)]
@@ -271,10 +283,10 @@ def measure_wall(blks, x, steps, warmup):
     settle(lambda: _lib.check(lib.lbmoe_forward(*calls[next(it) % len(calls)][2]), "lbmoe_forward"),
            warmup, SETTLE_S)
     t0 = time.perf_counter()
-    for i in range(steps):
-        lib.lbmoe_forward(*calls[i % len(calls)][2])
+    rcs = [lib.lbmoe_forward(*calls[i % len(calls)][2]) for i in range(steps)]
     torch.cuda.synchronize()
     us = (time.perf_counter() - t0) / steps * 1e6
+    check_all(rcs)
     L, ws, _ = calls[0]
     off, _ = _lib.workspace_region(L, T, "counts")
     counts = ws[off:off + 4 * L.num_experts].view(torch.int32).cpu()
@@ -317,7 +329,7 @@ def norm_config(name, shape, hid, res, nw, steps, dev, eps=1e-6):
     torch_norm()
     us_fused = timed(lambda: _lib.check(lib.lbmoe_forward_norm(*fused), "lbmoe_forward_norm"))
     us_plain = timed(lambda: _lib.check(lib.lbmoe_forward(*plain), "lbmoe_forward"))
-    us_torch = timed(lambda: (torch_norm(), lib.lbmoe_forward(*plain)))
+    us_torch = timed(lambda: (torch_norm(), _lib.check(lib.lbmoe_forward(*plain), "lbmoe_forward")))
     del blk
     return {"config": name, "T": T, "us_per_call_fused": round(us_fused, 1),
             "us_per_call_block_only": round(us_plain, 1),
@@ -389,7 +401,7 @@ def extra_configs(dev, steps, only=None, cpu_budget_s=0.0):
         for T, name in runs:
             x = make_x(g, T, shape.hidden_size, device=dev)
             if wanted(name):
-                n = steps if T <= 256 else max(3, steps // 5)
+                n = steps if T <= 256 else max(MIN_PREFILL_STEPS, steps // 5)
                 us, hit = measure_wall([blk], x, n, max(1, n // 5))
                 e = entry(name, shape, T, us, hit, 1 if fp8 else 2,
                           "mfma" if fp8 and T > 256 else "hbm")
@@ -461,7 +473,7 @@ def main():
     if not args.no_prefill:
         default_prefill = args.shape == "qwen3-30b-a3b" and args.prefill_T == 8192
         pblk, px = layer_inputs(shape, args.prefill_T, 0, True, dev)
-        steps = max(3, args.steps // 5)
+        steps = max(MIN_PREFILL_STEPS, args.steps // 5)
         p = measure(pblk, px, steps, max(1, args.warmup // 5), hip, SETTLE_S)
         plb, plf, pgb, pgf = work(shape, args.prefill_T, p["hit_experts"])
         pgu = p["stage_us"]["gate_up"]

@@ -17,9 +17,9 @@
  *  - Every entry point returns an lbmoe_status; a negative value means nothing was
  *    enqueued (argument errors) or the launch failed. There is no fallback path.
  *  - The library's only global state is set once per device and then read: the
- *    architecture check and the address of lbmoe_forward_static's workspace. Concurrent calls
- *    on different streams with different workspaces are independent; lbmoe_forward_static
- *    calls on one device share one workspace (see there).
+ *    architecture check, the device's CU count and the address of lbmoe_forward_static's
+ *    workspace. Concurrent calls on different streams with different workspaces are
+ *    independent; lbmoe_forward_static calls on one device share one workspace (see there).
  */
 #ifndef LBMOE_H
 #define LBMOE_H
@@ -144,8 +144,9 @@ int32_t lbmoe_forward_norm(const lbmoe_layer* layer, const void* hidden, const v
 int32_t lbmoe_pack_weights(const lbmoe_layer* layer, void* gate_up_tiled, void* down_tiled,
                            void* shared_gate_up_tiled, void* shared_down_tiled, void* stream);
 
-/* Bytes of the device workspace lbmoe_forward_static uses (one per GPU, held until the process
- * ends). */
+/* Bytes of the device workspace lbmoe_forward_static uses: one array per GPU, part of the
+ * library's device code, so every GPU that runs any of the library's kernels holds it until the
+ * process ends, whether or not lbmoe_forward_static is called. */
 #define LBMOE_STATIC_WORKSPACE_BYTES (64u << 20)
 
 /*

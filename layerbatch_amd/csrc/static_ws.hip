@@ -29,8 +29,16 @@ static int32_t scratch_of_current_device(void** out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LBMOE_ERR_DEVICE;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch[dev]) {
+    // The first call may come while the caller's stream is being captured into a graph: the
+    // lookup is not stream work, so this thread's capture mode is relaxed around it (a capture
+    // in the global or thread-local mode would otherwise refuse a runtime call that may load
+    // the code object) and restored afterwards.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return LBMOE_ERR_DEVICE;
     void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LBMOE_ERR_DEVICE;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return LBMOE_ERR_DEVICE;
+    if (e != hipSuccess || !p) return LBMOE_ERR_DEVICE;
     g_scratch[dev] = p;
   }
   *out = g_scratch[dev];

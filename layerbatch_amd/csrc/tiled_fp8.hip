@@ -18,6 +18,7 @@
 // workgroup's rows use; both are copied global -> LDS ahead of the ring's first stage.
 #include "common.hpp"
 #include "internal.hpp"
+#include "offsets.hpp"
 #include "tiled_shape.hpp"
 
 namespace lbmoe {
@@ -384,13 +385,10 @@ void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
 }  // namespace f8t
 
 bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows) {
-  // the copies address operands with 32-bit byte offsets from a weight matrix, xq or actq
-  const int64_t Imax = gw.I > gw.Is ? gw.I : gw.Is;
-  constexpr int64_t kMaxOffset = int64_t{1} << 32;
+  // the copies address operands with byte offsets below 2^31 from a weight matrix, xq or actq
   return tiled_supported(gw) && gw.H / 128 <= f8t::kMaxKBlocks &&
          gw.I / 128 <= f8t::kMaxKBlocks && gw.Is / 128 <= f8t::kMaxKBlocks &&
-         T * gw.H < kMaxOffset && rows * Imax < kMaxOffset &&
-         2 * Imax * gw.H < kMaxOffset;
+         fp8_tiled_offsets_fit(T, rows, gw.H, gw.I > gw.Is ? gw.I : gw.Is);
 }
 
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,

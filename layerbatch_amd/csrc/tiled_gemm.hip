@@ -39,8 +39,11 @@
 // a weight tile is one contiguous 32 KB block already in LDS order. HBM streams those blocks
 // markedly faster than 256 row segments of 128 bytes spread over 1 MB (a read probe in the
 // ring's pattern, with token copies that hit L2 as here: 6.7 against 5.2 TB/s).
+#include <atomic>
+
 #include "common.hpp"
 #include "internal.hpp"
+#include "offsets.hpp"
 #include "route_token.hpp"
 #include "tiled_shape.hpp"
 
@@ -1076,10 +1079,7 @@ bool tiled_supported(const GroupWeights& gw) {
 }
 
 bool tiled_offsets_fit(const GroupWeights& gw, int64_t T, int k) {
-  constexpr int64_t kMax = int64_t{1} << 31;
-  const int64_t imax = gw.I > gw.Is ? gw.I : gw.Is;
-  return T * gw.H * 2 < kMax && T * (k + 1) * imax * 2 < kMax &&
-         static_cast<int64_t>(imax) * gw.H * 2 < kMax;
+  return bf16_tiled_offsets_fit(T, k, gw.H, gw.I > gw.Is ? gw.I : gw.Is);
 }
 
 // Workgroups of a bf16 GEMM launch: one per possible item; the per-XCD rounding of the two item
@@ -1125,17 +1125,20 @@ hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, con
 }
 
 // CUs of the current device, rounded down to a multiple of 8 (every XCD the same number).
+// Looked up once per device; host threads that race on the first lookup store the same value.
 static int device_cus() {
   constexpr int kMaxDevices = 64;
-  static int cus[kMaxDevices];             // per device, looked up once (0: not yet)
+  static std::atomic<int> cus[kMaxDevices];   // per device (0: not yet looked up)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
-  if (cus[dev] == 0) {
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    cus[dev] = n >= 8 ? n / 8 * 8 : 8;
+    c = n >= 8 ? n / 8 * 8 : 8;
+    cus[dev].store(c, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return c;
 }
 
 // The persistent gate_up launch (one workgroup per CU) takes over from this many table entries

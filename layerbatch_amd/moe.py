@@ -32,6 +32,7 @@ kernels only (no host synchronisation), and raises RuntimeError for CPU tensors,
 or a missing library build.
 """
 import ctypes
+import warnings
 
 import torch
 from torch import nn
@@ -159,6 +160,27 @@ class Qwen3_5TopKRouter(nn.Module):
         return w, idx
 
 
+def _stamp(tensors):
+    """Identity of the tensors a tiled copy was packed from: storage address and version
+    counter (bumped by every in-place write, e.g. load_state_dict's copy_)."""
+    return tuple((t.data_ptr(), t._version) for t in tensors)
+
+
+def _tiled_current(owner, sources, what):
+    """Whether owner's tiled copies still match their source tensors. Stale copies (the
+    weights were replaced or written since pack_tiled_) are dropped with a warning: the
+    layer then streams the checkpoint tensors, whose results are identical."""
+    if owner.gate_up_tiled is None:
+        return False
+    if _stamp(sources) == owner.tiled_stamp:
+        return True
+    warnings.warn(f"{what} changed after pack_tiled_(): its tiled copies are dropped; call "
+                  "pack_tiled_() again to restore the faster prefill GEMMs", RuntimeWarning,
+                  stacklevel=3)
+    owner.gate_up_tiled = owner.down_tiled = owner.tiled_stamp = None
+    return False
+
+
 class Qwen3_5Experts(nn.Module):
     """Fused expert weights stored as 3-D tensors (qwen3_5.py:781-800).
 
@@ -178,6 +200,7 @@ class Qwen3_5Experts(nn.Module):
         self.weight_dtype = _lib.LBMOE_W_BF16
         self.gate_up_q = self.gate_up_scale = self.down_q = self.down_scale = None
         self.gate_up_tiled = self.down_tiled = None     # pack_tiled_ copies (bf16 only)
+        self.tiled_stamp = None                         # _stamp of their source tensors
 
     def fill_layer(self, L):
         L.num_experts = self.num_experts
@@ -197,7 +220,7 @@ class Qwen3_5Experts(nn.Module):
             _require_shape(self.down_proj, (E, H, I), "experts.down_proj")
             L.gate_up_proj = self.gate_up_proj.data_ptr()
             L.down_proj = self.down_proj.data_ptr()
-            if self.gate_up_tiled is not None:
+            if _tiled_current(self, (self.gate_up_proj, self.down_proj), "experts weights"):
                 L.gate_up_tiled = self.gate_up_tiled.data_ptr()
                 L.down_tiled = self.down_tiled.data_ptr()
 
@@ -239,6 +262,10 @@ class Qwen3_5SharedExpertMLP(nn.Module):
         self.weight_dtype = _lib.LBMOE_W_BF16
         self.q = None   # fp8: dict name -> (codes, scales)
         self.gate_up_tiled = self.down_tiled = None     # pack_tiled_ copies (bf16 only)
+        self.tiled_stamp = None                         # _stamp of their source tensors
+
+    def tiled_sources(self):
+        return (self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)
 
     def _ptrs(self):
         if self.weight_dtype == _lib.LBMOE_W_FP8_E4M3:
@@ -258,7 +285,8 @@ class Qwen3_5SharedExpertMLP(nn.Module):
         (g, u, d), (gs, us, ds) = self._ptrs()
         L.shared_gate_proj, L.shared_up_proj, L.shared_down_proj = g, u, d
         L.shared_gate_scale, L.shared_up_scale, L.shared_down_scale = gs, us, ds
-        if self.weight_dtype == _lib.LBMOE_W_BF16 and self.gate_up_tiled is not None:
+        if (self.weight_dtype == _lib.LBMOE_W_BF16
+                and _tiled_current(self, self.tiled_sources(), "shared_expert weights")):
             L.shared_gate_up_tiled = self.gate_up_tiled.data_ptr()
             L.shared_down_tiled = self.down_tiled.data_ptr()
 
@@ -392,8 +420,10 @@ class Qwen3_5SparseMoeBlock(nn.Module):
         """Derive the tiled copies of the bf16 expert weights (lbmoe_pack_weights), which the
         prefill-sized GEMMs stream faster than the checkpoint tensors; forward then passes both.
         The copies hold as many bytes as the expert weights again and are not updated when the
-        weights change: call this again after loading new weights. No counterpart in the
-        reference (a load-time layout step)."""
+        weights change: a later call that finds the weights replaced or written since (storage
+        address or version counter changed) drops the copies with a RuntimeWarning and streams
+        the checkpoint tensors (same results); call this again after loading new weights. No
+        counterpart in the reference (a load-time layout step)."""
         if self.experts.weight_dtype != _lib.LBMOE_W_BF16:
             raise RuntimeError("pack_tiled_ needs bf16 expert weights")
         ex, se = self.experts, self.shared_expert
@@ -415,8 +445,10 @@ class Qwen3_5SparseMoeBlock(nn.Module):
                                            ptr(sdn) if sdn is not None else None,
                                            _lib.stream_of(dev)), "lbmoe_pack_weights")
         ex.gate_up_tiled, ex.down_tiled = gu, dn
+        ex.tiled_stamp = _stamp((ex.gate_up_proj, ex.down_proj))
         if se is not None:
             se.gate_up_tiled, se.down_tiled = sgu, sdn
+            se.tiled_stamp = _stamp(se.tiled_sources())
         return self
 
     @torch.no_grad()

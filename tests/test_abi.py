@@ -30,8 +30,8 @@ def test_library_exports_every_declared_entry_point(lbmoe):
     assert lbmoe.lbmoe_abi_version() == 2
 
 
-def test_struct_layout_matches_header(tmp_path):
-    fields = [f for f, _ in _lib.LbmoeLayer._fields_]
+def _header_layout(fields, tmp_path):
+    """sizeof(lbmoe_layer) and offsetof of each named field, from gcc on include/lbmoe.h."""
     src = tmp_path / "probe.c"
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
              "int main(void) {", '  printf("%zu\\n", sizeof(lbmoe_layer));']
@@ -42,9 +42,54 @@ def test_struct_layout_matches_header(tmp_path):
     subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
     vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
                                            check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(_lib.LbmoeLayer)
-    for f, off in zip(fields, vals[1:]):
-        assert getattr(_lib.LbmoeLayer, f).offset == off, f
+    return vals[0], vals[1:]
+
+
+def _assert_struct_matches_header(cls, tmp_path):
+    fields = [f for f, _ in cls._fields_]
+    size, offsets = _header_layout(fields, tmp_path)
+    assert ctypes.sizeof(cls) == size, f"{cls.__name__}: {ctypes.sizeof(cls)} bytes, header {size}"
+    for f, off in zip(fields, offsets):
+        assert getattr(cls, f).offset == off, f
+
+
+def test_struct_layout_matches_header(tmp_path):
+    _assert_struct_matches_header(_lib.LbmoeLayer, tmp_path)
+
+
+def _integration_stub():
+    """The ctypes stub that INTEGRATION.md gives maintainers: its LbmoeLayer class and the
+    lbmoe_forward argtypes, evaluated from the document's own code block."""
+    import ast
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```python\n(.*?)```", text, re.S)
+    code = [b for b in blocks if "class LbmoeLayer(ctypes.Structure)" in b]
+    assert len(code) == 1, "INTEGRATION.md must hold exactly one ctypes stub"
+    tree = ast.parse(code[0])
+    ns = {"ctypes": ctypes}
+    cls = next(n for n in tree.body if isinstance(n, ast.ClassDef) and n.name == "LbmoeLayer")
+    exec(compile(ast.Module(body=[cls], type_ignores=[]), "INTEGRATION.md", "exec"), ns)
+    argtypes = None
+    for n in tree.body:
+        if (isinstance(n, ast.Assign) and isinstance(n.targets[0], ast.Attribute)
+                and ast.unparse(n.targets[0]) == "lib.lbmoe_forward.argtypes"):
+            argtypes = eval(compile(ast.Expression(body=n.value), "INTEGRATION.md", "eval"), ns)
+    return ns["LbmoeLayer"], argtypes
+
+
+def test_integration_stub_matches_header(tmp_path):
+    """A maintainer who copies INTEGRATION.md's stub gets the header's struct: every field, in
+    order, at the header's offsets, with the header's size (a short struct would let the library
+    read past the caller's object), and lbmoe_forward's argument list."""
+    stub, argtypes = _integration_stub()
+    assert [f for f, _ in stub._fields_] == [f for f, _ in _lib.LbmoeLayer._fields_]
+    _assert_struct_matches_header(stub, tmp_path)
+    assert argtypes is not None, "the stub must declare lbmoe_forward.argtypes"
+    want = [ctypes.POINTER(stub), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    assert len(argtypes) == len(want)
+    for a, b in zip(argtypes[1:], want[1:]):
+        assert a is b
 
 
 def _layer(**kw):
@@ -170,3 +215,66 @@ def test_modules_refuse_cpu_tensors():
         "experts.down_proj": (4, 256, 256), "shared_expert.gate_proj.weight": (128, 256),
         "shared_expert.up_proj.weight": (128, 256), "shared_expert.down_proj.weight": (256, 128),
         "shared_expert_gate.weight": (1, 256)}
+
+
+def test_tiled_offset_limits_at_the_2_31_boundary(tmp_path):
+    """The LDS-tiled GEMMs copy operands through buffer resources whose range ends below 2^31
+    bytes; a copy past it reads zeros. The host predicates (csrc/offsets.hpp) must refuse any
+    batch whose operand matrices reach 2^31 bytes, so those take the 64-bit streaming GEMMs."""
+    hdr = os.path.join(ROOT, "layerbatch_amd", "csrc", "offsets.hpp")
+    cases = [
+        # fp8: xq [T, H] bytes, actq [rows, Imax] bytes, one expert's gate_up [2*Imax, H] bytes
+        ("fp8", (1 << 20) - 1, 1 << 10, 2048, 512, True),
+        ("fp8", 1 << 20, 1 << 10, 2048, 512, False),          # xq = 2^31 bytes
+        ("fp8", 1 << 10, (1 << 22) - 1, 2048, 512, True),
+        ("fp8", 1 << 10, 1 << 22, 2048, 512, False),          # actq = 2^31 bytes
+        ("fp8", 1 << 10, 1 << 10, 1 << 14, 1 << 16, False),   # gate_up = 2^31 bytes
+        # Qwen3-30B-A3B fp8 (k = 8, I = 768): actq rows T*8 reach 2^31 / 768 at T = 349,526
+        ("fp8", 349525, 349525 * 8, 2048, 768, True),
+        ("fp8", 349526, 349526 * 8, 2048, 768, False),
+        # bf16: x [T, H] * 2, act [T*(k+1), Imax] * 2, one expert matrix [Imax, H] * 2
+        ("bf16", (1 << 19) - 1, 0, 2048, 128, True),
+        ("bf16", 1 << 19, 0, 2048, 128, False),               # x = 2^31 bytes
+        ("bf16", 155344, 8, 2048, 768, True),                 # act = 2,147,475,456 bytes
+        ("bf16", 155345, 8, 2048, 768, False),
+        ("bf16", 16, 8, 1 << 15, 1 << 15, False),             # expert matrix = 2^31 bytes
+    ]
+    src = tmp_path / "offsets_probe.cpp"
+    lines = ["#include <cstdio>", f'#include "{hdr}"', "int main() {"]
+    for kind, a, b, H, imax, _ in cases:
+        fn = "fp8_tiled_offsets_fit" if kind == "fp8" else "bf16_tiled_offsets_fit"
+        lines.append(f'  std::printf("%d\\n", (int)lbmoe::{fn}({a}LL, {b}LL, {H}LL, {imax}LL));')
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "offsets_probe"
+    subprocess.run(["g++", "-std=c++17", str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    for case, g in zip(cases, got):
+        assert bool(int(g)) == case[-1], case
+
+
+def test_stale_tiled_copies_are_dropped():
+    """pack_tiled_'s copies remember their source tensors (address and version counter): once a
+    weight is written in place (load_state_dict's copy_) or replaced, the next call drops the
+    copies with a warning instead of streaming stale weights in prefill-sized batches."""
+    import warnings
+    import torch
+    from layerbatch_amd import moe
+    ex = moe.Qwen3_5Experts(4, 256, 256)
+    src = (ex.gate_up_proj, ex.down_proj)
+    for replace in (False, True):
+        ex.gate_up_tiled, ex.down_tiled = torch.zeros(1), torch.zeros(1)
+        ex.tiled_stamp = moe._stamp(src)
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")
+            assert moe._tiled_current(ex, src, "experts weights")
+        with torch.no_grad():
+            if replace:
+                ex.down_proj = torch.nn.Parameter(torch.zeros_like(ex.down_proj))
+                src = (ex.gate_up_proj, ex.down_proj)
+            else:
+                ex.gate_up_proj.copy_(torch.ones_like(ex.gate_up_proj))
+        with pytest.warns(RuntimeWarning, match="pack_tiled_"):
+            assert not moe._tiled_current(ex, src, "experts weights")
+        assert ex.gate_up_tiled is None and ex.down_tiled is None
+        assert not moe._tiled_current(ex, src, "experts weights")   # dropped: no second warning

@@ -15,7 +15,7 @@ import torch
 from layerbatch_amd.synth import SHAPES, make_layer, make_x, zipf_bias
 from oracle import moe as om
 from tests import gpu_checks as gc
-from tests.helpers import bf16_bits_of, to_np
+from tests.helpers import bf16_bits_of, scale_blocks_pow2, scale_groups_pow2, to_np
 from tests.test_gpu_parity import _block, _region
 
 pytestmark = pytest.mark.gpu
@@ -66,9 +66,17 @@ def tile_rows(counts, offsets, perm_tok):
     return np.unique(np.concatenate(pos)) if pos else np.zeros(0, np.int64)
 
 
-def _run_full(shape, T, device, seed, zipf, sample=256, fp8=False):
+def _run_full(shape, T, device, seed, zipf, sample=256, fp8=False, patterned=False):
     w, g = make_layer(shape, seed=seed, device=device)
     x = make_x(g, T, shape.hidden_size, device=device)
+    if patterned:
+        # every 128x128 weight block scale and every (token, 128-channel) activation scale
+        # differs from its neighbours by a power of two, so a kernel reading a neighbouring
+        # block's or group's scale lands far outside the tolerance
+        for k_ in ("gate_up", "down", "sh_gate", "sh_up", "sh_down"):
+            if k_ in w:
+                w[k_] = scale_blocks_pow2(w[k_])
+        x = scale_groups_pow2(x)
     blk = _block(shape, w, device)
     if zipf:
         blk.gate.logit_bias = zipf_bias(g, shape.num_experts, device=device)
@@ -112,6 +120,17 @@ def _run_full(shape, T, device, seed, zipf, sample=256, fp8=False):
             gsh = om.shared_gate(xn[rows], to_np(w["sh_gate_w"])).astype(np.float64)
             y_ref = y_ref + gsh[:, None] * om.shared_expert_fp8(xn[rows], *q)
         tol = gc.TOL_FP8
+        if patterned:
+            # the pattern's power at this shape: the oracle itself, handed every weight block's
+            # k-neighbour scale, lands far outside the tolerance (on 16 of the rows)
+            r16 = rows[:16]
+            su, sd = ex.gate_up_scale.cpu().numpy(), ex.down_scale.cpu().numpy()
+            y16 = om.experts_fp8(xn[r16], idx_ref[r16], to_np(topw)[r16], _Experts(ex.gate_up_q), su,
+                                 _Experts(ex.down_q), sd)
+            shifted = om.experts_fp8(xn[r16], idx_ref[r16], to_np(topw)[r16],
+                                     _Experts(ex.gate_up_q), np.roll(su, 1, axis=-1),
+                                     _Experts(ex.down_q), np.roll(sd, 1, axis=-1))
+            assert om.rel_err(shifted, y16) > 10 * tol
     else:
         y_ref = om.experts(xn[rows], idx_ref[rows], tw, _Experts(w["gate_up"]), _Experts(w["down"]))
         if shared:
@@ -158,3 +177,12 @@ def test_fullsize_e512_shared(gpu, T):
 def test_fullsize_e512_fp8(gpu, T):
     """The E=512 layer with e4m3 weights and activations (per-block fp32 scales)."""
     _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=3, zipf=False, fp8=True)
+
+
+@pytest.mark.parametrize("T", [128, 16384])
+def test_fullsize_e512_fp8_scale_patterns(gpu, T):
+    """The E=512 fp8 layer at its full shape (16 gate_up and 4 down k-tiles of 128, the shared
+    expert's own scale rows) with patterned block and group scales: the streaming GEMMs at
+    T=128, the LDS-tiled ones at T=16384."""
+    print(f"fp8 E=512 patterned scales T={T}", flush=True)
+    _run_full(SHAPES["qwen3-next-e512"], T, gpu, seed=T + 9, zipf=False, fp8=True, patterned=True)

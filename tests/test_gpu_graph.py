@@ -81,11 +81,13 @@ def test_repeated_calls_are_deterministic(gpu):
     assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
 
 
-# the toy layer at the engine's small buckets, and the Qwen3-30B-A3B layer up to 256; the
-# replays of the buckets named last are also checked against the float64 oracle
+# the toy layer at the engine's small buckets, and the Qwen3-30B-A3B layer up to the engine's
+# largest bucket, 512 (model_runner.py:1466, :1480; max_num_seqs 512, config.py:183): from 448 on
+# (28 tokens per expert) its replays run the LDS-tiled GEMMs. The replays of the buckets named
+# last are also checked against the float64 oracle.
 @pytest.mark.parametrize("shape,buckets,checked", [
     (SHAPE, [1, 2, 4, 8, 16, 32, 48, 64], [48]),
-    (SHAPES["qwen3-30b-a3b"], [1, 8, 16, 64, 128, 256], [128, 256])])
+    (SHAPES["qwen3-30b-a3b"], [1, 8, 16, 64, 128, 256, 384, 448, 512], [128, 256, 448, 512])])
 def test_decode_bucket_graphs(gpu, shape, buckets, checked):
     """The engine's decode capture (model_runner.py:1463-1507): one graph per batch bucket,
     captured from the largest bucket down in a shared memory pool, all reading slices of one
@@ -111,6 +113,7 @@ def test_decode_bucket_graphs(gpu, shape, buckets, checked):
         graphs[bs] = graph
         torch.cuda.synchronize()
     for bs in buckets:
+        print(f"bucket {bs}: replay", flush=True)
         live = max(1, bs - 1 - bs // 4)                          # a partly filled bucket
         x = make_x(g, live, H, device=gpu)
         static_x.zero_()
@@ -133,3 +136,45 @@ def test_decode_bucket_graphs(gpu, shape, buckets, checked):
         y_e = blk(static_x[:bs].clone())
         torch.cuda.synchronize()
         assert torch.equal(outputs[:bs], y_e), f"bucket {bs} replay differs from the eager result"
+
+
+# Two decoder layers' blocks (different weights) on two streams, as LayerBatch decode runs group
+# A's unit t on la_stream while group B's unit t-1 runs on fa_stream (layer_batch.py:175-212):
+# decode-sized batches (weight-streaming GEMMs, the permutation inside gate_up), prefill-sized
+# ones (LDS-tiled GEMMs with the persistent gate_up's work queues in the workspace), and the fp8
+# E=512 layer with its shared expert.
+@pytest.mark.parametrize("name,Ta,Tb,fp8", [("qwen3-30b-a3b", 48, 80, False),
+                                          ("qwen3-30b-a3b", 1024, 2048, False),
+                                          ("qwen3-next-e512", 128, 600, True)])
+def test_two_streams_overlapping_calls(gpu, name, Ta, Tb, fp8):
+    """Calls on two streams with one workspace each and no synchronisation between the
+    streams give, bit for bit, the outputs of the same calls made one after another."""
+    print(f"two streams: {name} T={Ta} and T={Tb} fp8={fp8}", flush=True)
+    shape = SHAPES[name]
+    blks, xs = [], []
+    for seed, T in ((31, Ta), (32, Tb)):
+        w, g = make_layer(shape, seed=seed, device=gpu)
+        blk = _block(shape, w, gpu)
+        if fp8:
+            blk.quantize_fp8_()
+        del w
+        blks.append(blk)
+        xs.append([make_x(g, T, shape.hidden_size, device=gpu) for _ in range(4)])
+    ref = [[blk(x) for x in xl] for blk, xl in zip(blks, xs)]          # one after another
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [torch.empty(blk.workspace_size(xl[0].shape[0]), dtype=torch.uint8, device=gpu)
+           for blk, xl in zip(blks, xs)]
+    outs = [[torch.empty_like(x) for x in xl] for xl in xs]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rnd in range(2):
+        for i in range(4):                      # interleaved issue: both streams always busy
+            for j in (0, 1):
+                with torch.cuda.stream(streams[j]):
+                    outs[j][i].copy_(blks[j](xs[j][i], workspace=wss[j]))
+    for s in streams:
+        s.synchronize()
+    for j in (0, 1):
+        for i in range(4):
+            assert torch.equal(outs[j][i], ref[j][i]), f"stream {j} call {i} differs"

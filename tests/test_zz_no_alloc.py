@@ -3,6 +3,9 @@ equals lbmoe_forward's bit for bit, on consecutive calls that reuse the library'
 workspace with a smaller batch second, and calls past the workspace's limit are refused on the
 host before anything is enqueued."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -49,7 +52,7 @@ def test_static_matches_workspace_forward(gpu, shape, T1, T2, fp8):
         y = _forward_static(blk, x)
         torch.cuda.synchronize()
         assert torch.equal(y, y_ref), f"T={T}: static-workspace output differs from lbmoe_forward"
-        # a call of the other kind in between leaves the next static call unaffected
+        # a second static call finds the first one's intermediates in the array: same output
         y2 = _forward_static(blk, x)
         torch.cuda.synchronize()
         assert torch.equal(y2, y_ref), f"T={T}: repeated static call differs"
@@ -75,3 +78,55 @@ def test_static_limit_refused_on_host(lbmoe):
     bad = _lib.LbmoeLayer()
     bad.hidden_size = 1000
     assert lbmoe.lbmoe_forward_static(ctypes.byref(bad), p, 4, p, None) == -2
+
+
+# Run in a fresh process, so that the library's first lbmoe_forward_static call on the device
+# (which looks up the array's address) happens inside the graph capture.
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from layerbatch_amd import _lib
+from layerbatch_amd.synth import MoEShape, make_layer, make_x
+from tests.test_gpu_parity import _block
+dev = torch.device("cuda:0")
+shape = MoEShape(1024, 16, 2, 512, 256)
+w, g = make_layer(shape, seed=4, device=dev)
+blk = _block(shape, w, dev)
+L = blk.layer()
+lib = _lib.lib()
+T = 64
+static_x = make_x(g, T, 1024, device=dev)
+static_y = torch.empty_like(static_x)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    rc = lib.lbmoe_forward_static(ctypes.byref(L), _lib.ptr(static_x), T, _lib.ptr(static_y),
+                                  _lib.stream_of(dev))
+_lib.check(rc, "lbmoe_forward_static under capture")
+ws = torch.empty(_lib.workspace_size(L, T), dtype=torch.uint8, device=dev)
+for rep in range(3):
+    x = make_x(g, T, 1024, device=dev)
+    static_x.copy_(x)
+    graph.replay()
+    torch.cuda.synchronize()
+    y = torch.empty_like(x)
+    _lib.check(lib.lbmoe_forward(ctypes.byref(L), _lib.ptr(x), T, _lib.ptr(y), _lib.ptr(ws),
+                                 ws.numel(), _lib.stream_of(dev)), "lbmoe_forward")
+    torch.cuda.synchronize()
+    assert torch.equal(static_y, y), f"replay {rep} differs from lbmoe_forward"
+    print(f"replay {rep}: equal to lbmoe_forward", flush=True)
+print("CAPTURE_OK", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_static_first_call_inside_graph_capture(gpu):
+    """The entry point is meant for code under graph capture: its first call on a device,
+    which looks up the array's address, is made inside torch.cuda.graph capture in a fresh
+    process; three replays, with eager lbmoe_forward calls between them, each equal
+    lbmoe_forward's output bit for bit."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("static workspace: first call inside graph capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-u", "-c", _CAPTURE_SCRIPT, root], capture_output=True,
+                       text=True, timeout=110, cwd=root)
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, (r.stdout[-2000:], r.stderr[-3000:])
