@@ -928,7 +928,8 @@ void router_route_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
     const float v = bf2f(sl[tr * kStride + ec]) + (bias ? bias[ec] : 0.f);
     z[j] = (!(v == v) || e >= E) ? -INFINITY : v;             // a NaN logit is never preferred
   }
-  route_select8<EPG>(z, E, k, static_cast<int64_t>(t0 + tl) * k, ok, idx, topw, s_idx + tr * k);
+  route_select8<EPG>(z, E, k, static_cast<int64_t>(t0 + tl) * k, ok, idx, topw, s_idx + tr * k,
+                     bias == nullptr);
   __syncthreads();
   const int nchunks = k * nb;
   for (int s = w; s < k; s += kWaves) {

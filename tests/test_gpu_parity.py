@@ -41,8 +41,12 @@ def _region(blk, ws, T, name, dtype, shape):
 
 
 def _run_and_check(shape, T, device, seed=0, bias=None, gen_device="cpu", sample=None,
-                   pack=False):
+                   pack=False, gate_rows_mod=None):
     w, g = make_layer(shape, seed=seed, device=gen_device)
+    if gate_rows_mod:
+        # router row e repeats row e mod gate_rows_mod: groups of experts get identical logits,
+        # so most selections are decided by the tie rule (lower expert index first)
+        w["gate"] = w["gate"][torch.arange(shape.num_experts) % gate_rows_mod].contiguous()
     x = make_x(g, T, shape.hidden_size, device=gen_device)
     wd = {k_: v.to(device) for k_, v in w.items()}
     blk = _block(shape, wd, device)
@@ -167,6 +171,20 @@ def test_block_prefill_route_in_router(gpu, shape, T, zipf):
     if zipf:
         bias = zipf_bias(torch.Generator().manual_seed(shape.num_experts), shape.num_experts)
     _run_and_check(shape, T, gpu, seed=T, bias=bias, sample=96)
+
+
+# Ties between whole experts: router rows repeated, no bias, so selection runs on packed keys
+# (every score a bf16 value) and equal logits are ordered by expert index: selection inside the
+# tiled router (T >= 1024, E <= 128: 8-lane groups), the selection kernel of E = 512 prefill and
+# decode, and the small-batch kernels.
+@pytest.mark.parametrize("shape,T,mod", [(MoEShape(512, 128, 8, 256, 0), 2048, 16),
+                                         (MoEShape(512, 100, 6, 256, 0), 1100, 7),
+                                         (MoEShape(512, 512, 10, 256, 256), 1024, 50),
+                                         (MoEShape(512, 512, 10, 256, 256), 100, 3),
+                                         (MoEShape(512, 128, 8, 256, 0), 3, 5),
+                                         (MoEShape(512, 128, 8, 256, 0), 12, 9)])
+def test_route_tied_router_rows(gpu, shape, T, mod):
+    _run_and_check(shape, T, gpu, seed=T + mod, sample=96, gate_rows_mod=mod)
 
 
 # Tiled-layout copies of the expert weights (lbmoe_pack_weights): the prefill GEMMs read them
