@@ -178,3 +178,4 @@ def test_two_streams_overlapping_calls(gpu, name, Ta, Tb, fp8):
     for j in (0, 1):
         for i in range(4):
             assert torch.equal(outs[j][i], ref[j][i]), f"stream {j} call {i} differs"
+
