@@ -221,6 +221,13 @@ bool tiled_supported(const GroupWeights& gw);
 // Whether every byte offset of the bf16 tiled GEMMs' buffer copies stays below 2^31 for a call
 // of T tokens (x, the act rows of the routed and shared experts, one expert's weight matrix).
 bool tiled_offsets_fit(const GroupWeights& gw, int64_t T, int k);
+// CUs of the current device, rounded down to a multiple of 8 (every XCD the same number).
+int device_cus();
+// The persistent gate_up launches (one workgroup per CU) take over from this many table entries
+// per CU: with fewer items per CU the in-order hardware dispatch leaves little idle and the
+// persistent loop's per-item queue work costs more than it saves (bf16 Qwen3-30B-A3B T=1024:
+// 3.8 entries per CU, 2-5 us slower).
+constexpr int kPersistentMinEntriesPerCu = 6;
 // rows = routed + shared rows of the call
 bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows);
 hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, const GroupWeights& gw,

@@ -49,7 +49,10 @@ __device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
 // (dst_ld bytes per row) and dst_sc the group scales (dst_ld / 128 per row). Else out[row, h]
 // (bf16, dst_ld per row) over K = Ig. row0: the group's first row in src (down) / dst. src_sc:
 // per (row, 128 k) activation scales of src, src_ld / 128 per row.
-template <bool GATEUP, class S>
+// PERSIST: called from the persistent kernel's item loop, where the thread index goes through
+// an empty asm, so the per-lane arithmetic is redone per item rather than hoisted out of the loop
+// and held in registers across it.
+template <bool GATEUP, class S, bool PERSIST = false>
 __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
                                                  const uint8_t* __restrict__ src,
                                                  const float* __restrict__ src_sc, int src_ld,
@@ -72,8 +75,10 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
   const int nk = K / 128;                        // k-tiles = scale blocks
   const int c0 = wt * (GATEUP ? kWM / 2 : kWM);  // first channel / output column
 
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tid = threadIdx.x;
+  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w % kWavesM, wn = w / kWavesM;
 
   // Weights and the two weight-scale rows (nk floats each) of the workgroup's rows. gate_up:
@@ -339,15 +344,15 @@ __device__ __forceinline__ void tile_product_fp8(const GroupWeights& gw,
     // independent chains (LDS read, row maximum, divisions) overlap; tokens past the group's
     // rows are computed from whatever the staging area holds and not stored.
     uint8_t* q = static_cast<uint8_t*>(dst);
-    const int sub = threadIdx.x & 15;
+    const int sub = tid & 15;
     constexpr int kPer = kThreads / 16, kIters = kWT / kPer;
     static_assert(kWT % kPer == 0, "tokens per pass divide the tile");
     u32x4 v[kIters];
 #pragma unroll
-    for (int i = 0; i < kIters; ++i) v[i] = lds[staged_slot<kCols>((threadIdx.x >> 4) + i * kPer, sub)];
+    for (int i = 0; i < kIters; ++i) v[i] = lds[staged_slot<kCols>((tid >> 4) + i * kPer, sub)];
 #pragma unroll
     for (int i = 0; i < kIters; ++i) {
-      const int p = r0 + (threadIdx.x >> 4) + i * kPer;
+      const int p = r0 + (tid >> 4) + i * kPer;
       float sc;
       const u32x2 c = quant_group16(v[i], sc);
       if (p < n) {
@@ -382,6 +387,41 @@ void tiled_fp8_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
                                    it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
 }
 
+// gate_up as one workgroup per CU taking entries from the per-XCD work queues of the dispatch
+// table (queue_fetch): thread 0 claims the next entry once the previous item's stores have gone
+// out, and the barrier after it also orders the item's staging reads before the next fill.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tiled_fp8_persistent_kernel(GroupWeights gw, const uint8_t* __restrict__ src,
+                                 const float* __restrict__ src_sc, int src_ld,
+                                 const int32_t* __restrict__ perm_tok,
+                                 const u32x4* __restrict__ table, int slots, int* __restrict__ q,
+                                 void* __restrict__ dst, int dst_ld, float* __restrict__ dst_sc) {
+  __shared__ u32x4 lds[kRingU4];
+  __shared__ float scl[kActScales + kWScales];
+  __shared__ u32x4 ent;
+  __shared__ int tried;                // the queue state lives in LDS, not across the loop
+  if (threadIdx.x == 0) tried = 0;
+  for (;;) {
+    if (threadIdx.x == 0) {
+      WorkQueue wq{table, slots, q, static_cast<int>(blockIdx.x & 7), tried, 0};
+      ent = queue_fetch(wq);
+      tried = wq.tried;
+    }
+    __syncthreads();
+    const TileItem it = decode_item(ent);
+    if (it.g < 0) break;               // the same for the whole workgroup
+    if (it.tiny)
+      tile_product_fp8<true, Tiny, true>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                         it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
+    else if (it.narrow)
+      tile_product_fp8<true, Narrow, true>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                           it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
+    else
+      tile_product_fp8<true, Wide, true>(gw, src, src_sc, src_ld, perm_tok, it.g, it.r0, it.n,
+                                         it.row0, it.wt, dst, dst_ld, dst_sc, lds, scl);
+  }
+}
+
 }  // namespace f8t
 
 bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows) {
@@ -394,9 +434,18 @@ bool tiled_fp8_supported(const GroupWeights& gw, int64_t T, int64_t rows) {
 hipError_t launch_gate_up_tiled_fp8(const GroupWeights& gw, const void* xq, const float* xs,
                                     const int32_t* perm_tok, const int32_t* tiles, int max_tiles,
                                     int act_ld, void* actq, float* acts, hipStream_t s) {
-  f8t::tiled_fp8_kernel<true><<<tiled_grid(gw, max_tiles, true), kThreads, 0, s>>>(
-      gw, static_cast<const uint8_t*>(xq), xs, gw.H, perm_tok,
-      tiled_table(gw, tiles, max_tiles, true), actq, act_ld, acts);
+  const int grid = tiled_grid(gw, max_tiles, true), cus = device_cus();
+  const u32x4* table = tiled_table(gw, tiles, max_tiles, true);
+  if (grid >= kPersistentMinEntriesPerCu * cus) {
+    int32_t* q = queue_base(const_cast<int32_t*>(tiles), max_tiles, grid,
+                            tiled_grid(gw, max_tiles, false));
+    f8t::tiled_fp8_persistent_kernel<<<cus, kThreads, 0, s>>>(
+        gw, static_cast<const uint8_t*>(xq), xs, gw.H, perm_tok, table, grid / 8, q, actq, act_ld,
+        acts);
+  } else {
+    f8t::tiled_fp8_kernel<true><<<grid, kThreads, 0, s>>>(
+        gw, static_cast<const uint8_t*>(xq), xs, gw.H, perm_tok, table, actq, act_ld, acts);
+  }
   return hipGetLastError();
 }
 

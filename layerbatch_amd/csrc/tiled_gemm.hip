@@ -136,18 +136,6 @@ __device__ __forceinline__ int dispatch_item(int b, int W, int N) {
   return upto > before ? W + n0 + before : w0 + (j - before);
 }
 
-// Words of the tile list before the dispatch tables (entries, counts), rounded to 16 bytes.
-__host__ __device__ constexpr int64_t table_base(int max_tiles) {
-  return (2 * static_cast<int64_t>(max_tiles) + kTileListTail + 3) / 4 * 4;
-}
-
-// Work queues of the persistent gate_up launch, behind both dispatch tables: 8 counters (one per
-// XCD, 64 ints apart so that they sit on different cache lines), then the 8 queue lengths.
-constexpr int kQueueInts = 8 * 64 + 8;
-__host__ __device__ inline int32_t* queue_base(int32_t* tiles, int max_tiles, int grid_gu,
-                                               int grid_dn) {
-  return tiles + table_base(max_tiles) + 4 * static_cast<int64_t>(grid_gu + grid_dn);
-}
 
 // One entry of a dispatch table: the work of workgroup b of a bf16 GEMM launch, read with a
 // single 16-byte load: {group | weight tile << 16 (-1: none), first row | narrow flag,
@@ -375,40 +363,6 @@ __global__ __launch_bounds__(1024) void perm_scatter_build_kernel(
 // kRouter: logits[t, e] = x[t] . Wg[e] (gw.gate_up holds the router weight, gw.E its rows).
 enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 
-// Work queue of a persistent workgroup. XCD x's queue holds the dispatch-table entries
-// table[j * 8 + x], j < its length (the items a launch of one workgroup per entry would run on
-// that XCD, in the same order); its counter hands them out. A workgroup takes entries from its
-// home XCD's queue and, once that is empty, from the others in turn, so the last items of a
-// slow XCD spread over the chip.
-struct WorkQueue {
-  const u32x4* table;
-  int slots;       // table entries per XCD
-  int* q;          // counters q[x * 64], lengths q[8 * 64 + x]
-  int home;        // this workgroup's XCD
-  int tried;       // queues found empty so far
-  int own_len;     // length of the home queue
-};
-
-// Next entry (thread 0 only), synchronously: a queue whose counter has reached its length is
-// passed by with a load, otherwise an atomic takes an entry or finds the queue exhausted, so a
-// workgroup makes at most (entries taken + idle entries + 8) atomics.
-__device__ __forceinline__ u32x4 queue_fetch(WorkQueue& wq) {
-  while (wq.tried < 8) {
-    const int x = (wq.home + wq.tried) & 7;
-    int* cnt = wq.q + x * 64;
-    const int len = min(wq.q[8 * 64 + x], wq.slots);
-    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < len) {
-      const int j = atomicAdd(cnt, 1);
-      if (j < len) {
-        const u32x4 e = wq.table[j * 8 + x];
-        if (static_cast<int>(e[0]) >= 0) return e;
-        continue;                                  // an idle entry: the queue's next one
-      }
-    }
-    ++wq.tried;
-  }
-  return u32x4{0xffffffffu, 0u, 0u, 0u};
-}
 
 // Rows r0 .. r0 + S::kWT - 1 (clipped to n) of group g (a routed expert, or the shared
 // expert when g == gw.E), output columns of weight tile wt. row0: the group's first row in
@@ -1127,7 +1081,7 @@ hipError_t launch_build_tiles(const int32_t* counts, const int32_t* offsets, con
 
 // CUs of the current device, rounded down to a multiple of 8 (every XCD the same number).
 // Looked up once per device; host threads that race on the first lookup store the same value.
-static int device_cus() {
+int device_cus() {
   constexpr int kMaxDevices = 64;
   static std::atomic<int> cus[kMaxDevices];   // per device (0: not yet looked up)
   int dev = 0;
@@ -1146,7 +1100,6 @@ static int device_cus() {
 // per CU: with fewer items per CU the in-order hardware dispatch leaves little idle and the
 // persistent loop's per-item queue work costs more than it saves (Qwen3-30B-A3B T=1024: 3.8
 // entries per CU, 2-5 us slower).
-constexpr int kPersistentMinEntriesPerCu = 6;
 
 hipError_t launch_gate_up_tiled(const GroupWeights& gw, const void* x, const int32_t* perm_tok,
                                 const int32_t* tiles, int max_tiles, int64_t T, int act_ld,

@@ -116,6 +116,54 @@ __device__ __forceinline__ void store_staged(const u32x4* __restrict__ st, uint1
   }
 }
 
+// Words of the tile list before the dispatch tables (entries, counts), rounded to 16 bytes.
+__host__ __device__ constexpr int64_t table_base(int max_tiles) {
+  return (2 * static_cast<int64_t>(max_tiles) + kTileListTail + 3) / 4 * 4;
+}
+
+// Work queues of the persistent gate_up launch, behind both dispatch tables: 8 counters (one per
+// XCD, 64 ints apart so that they sit on different cache lines), then the 8 queue lengths.
+constexpr int kQueueInts = 8 * 64 + 8;
+__host__ __device__ inline int32_t* queue_base(int32_t* tiles, int max_tiles, int grid_gu,
+                                               int grid_dn) {
+  return tiles + table_base(max_tiles) + 4 * static_cast<int64_t>(grid_gu + grid_dn);
+}
+
+// Work queue of a persistent workgroup. XCD x's queue holds the dispatch-table entries
+// table[j * 8 + x], j < its length (the items a launch of one workgroup per entry would run on
+// that XCD, in the same order); its counter hands them out. A workgroup takes entries from its
+// home XCD's queue and, once that is empty, from the others in turn, so the last items of a
+// slow XCD spread over the chip.
+struct WorkQueue {
+  const u32x4* table;
+  int slots;       // table entries per XCD
+  int* q;          // counters q[x * 64], lengths q[8 * 64 + x]
+  int home;        // this workgroup's XCD
+  int tried;       // queues found empty so far
+  int own_len;     // length of the home queue
+};
+
+// Next entry (thread 0 only), synchronously: a queue whose counter has reached its length is
+// passed by with a load, otherwise an atomic takes an entry or finds the queue exhausted, so a
+// workgroup makes at most (entries taken + idle entries + 8) atomics.
+__device__ __forceinline__ u32x4 queue_fetch(WorkQueue& wq) {
+  while (wq.tried < 8) {
+    const int x = (wq.home + wq.tried) & 7;
+    int* cnt = wq.q + x * 64;
+    const int len = min(wq.q[8 * 64 + x], wq.slots);
+    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < len) {
+      const int j = atomicAdd(cnt, 1);
+      if (j < len) {
+        const u32x4 e = wq.table[j * 8 + x];
+        if (static_cast<int>(e[0]) >= 0) return e;
+        continue;                                  // an idle entry: the queue's next one
+      }
+    }
+    ++wq.tried;
+  }
+  return u32x4{0xffffffffu, 0u, 0u, 0u};
+}
+
 // Host side: workgroups of a GEMM launch and its dispatch table within the tile list.
 int tiled_grid(const GroupWeights& gw, int max_tiles, bool gate_up);
 const u32x4* tiled_table(const GroupWeights& gw, const int32_t* tiles, int max_tiles,

@@ -168,3 +168,35 @@ def test_fp8_checkpoint_matches_quantize(gpu, tmp_path, T):
     y1, y2 = loaded(x), ref(x)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
+
+
+def test_fp8_prefill_persistent_gate_up(gpu):
+    """A batch whose fp8 gate_up table has at least 6 entries per CU (H=1024, E=64, top-8, I=768,
+    T=8192 under a Zipf bias: wide, narrow and tiny tiles, empty experts whose entries are idle),
+    so gate_up runs as the persistent work-queue kernel. The workspace starts as all-ones bytes
+    (e4m3 NaN codes and NaN scales), so an item the queues skipped leaves NaN in the output: every
+    row is checked against the fp8 oracle."""
+    from layerbatch_amd.synth import zipf_bias
+    shape = MoEShape(1024, 64, 8, 768, 0)
+    T, k = 8192, 8
+    w, g = make_layer(shape, seed=17)
+    x = make_x(g, T, shape.hidden_size)
+    bias = zipf_bias(torch.Generator().manual_seed(29), shape.num_experts)
+    blk = _block(shape, {k_: v.to(gpu) for k_, v in w.items()}, gpu)
+    blk.gate.logit_bias = bias.to(gpu)
+    blk.quantize_fp8_()
+    ws = torch.full((blk.workspace_size(T),), 255, dtype=torch.uint8, device=gpu)
+    y = blk(x.to(gpu), workspace=ws)
+    torch.cuda.synchronize()
+    idx = to_np(_region(blk, ws, T, "topk_idx", torch.int32, (T, k))).astype(np.int64)
+    topw = to_np(_region(blk, ws, T, "topk_w", torch.bfloat16, (T, k)))
+    gc.check_route(idx, bf16_bits_of(_region(blk, ws, T, "topk_w", torch.bfloat16, (T, k))),
+                   to_np(_region(blk, ws, T, "logits", torch.bfloat16, (T, shape.num_experts))),
+                   bias.numpy(), k)
+    ex = blk.experts
+    y_ref = om.experts_fp8(to_np(x), idx, topw, ex.gate_up_q.cpu().numpy(),
+                           ex.gate_up_scale.cpu().numpy(), ex.down_q.cpu().numpy(),
+                           ex.down_scale.cpu().numpy())
+    yn = to_np(y)
+    assert np.isfinite(yn).all(), "rows the gate_up queues skipped"
+    gc.check_output(yn, y_ref, gc.TOL_FP8)
