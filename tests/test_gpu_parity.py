@@ -111,10 +111,13 @@ def test_block_odd_shapes(gpu, shape, T):
     _run_and_check(shape, T, gpu, seed=T + shape.num_experts)
 
 
-def test_block_with_bias(gpu):
-    shape = MoEShape(1024, 64, 6, 256, 0)
+# a router bias; the second case adds a shared expert (the gate inside the selection) with
+# E = 48, three router tiles of 16 experts
+@pytest.mark.parametrize("shape,T", [(MoEShape(1024, 64, 6, 256, 0), 200),
+                                     (MoEShape(768, 48, 4, 256, 256), 150)])
+def test_block_with_bias(gpu, shape, T):
     g = torch.Generator().manual_seed(11)
-    _run_and_check(shape, 200, gpu, seed=5, bias=zipf_bias(g, 64))
+    _run_and_check(shape, T, gpu, seed=5, bias=zipf_bias(g, shape.num_experts))
 
 
 @pytest.mark.parametrize("T", [3072, 5000])
@@ -175,9 +178,10 @@ def test_block_prefill_route_in_router(gpu, shape, T, zipf):
 
 # Ties between whole experts: router rows repeated, no bias, so selection runs on packed keys
 # (every score a bf16 value) and equal logits are ordered by expert index: selection inside the
-# tiled router (T >= 1024, E <= 128: 8-lane groups), the selection kernel of E = 512 prefill and
-# decode, and the small-batch kernels.
+# tiled router (T >= 1024, E <= 128: 8-lane groups), inside the decode router (16 < T < 1024,
+# E <= 128), the selection kernel of E = 512 prefill and decode, and the small-batch kernels.
 @pytest.mark.parametrize("shape,T,mod", [(MoEShape(512, 128, 8, 256, 0), 2048, 16),
+                                         (MoEShape(512, 128, 8, 256, 0), 200, 11),
                                          (MoEShape(512, 100, 6, 256, 0), 1100, 7),
                                          (MoEShape(512, 512, 10, 256, 256), 1024, 50),
                                          (MoEShape(512, 512, 10, 256, 256), 100, 3),
