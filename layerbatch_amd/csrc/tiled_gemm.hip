@@ -1230,6 +1230,11 @@ hipError_t launch_router_logits_tiled(const void* x, const void* wg, int64_t T, 
                        ((E + RouterShapeTall::kRows - 1) / RouterShapeTall::kRows);
   if (tall >= kRouterTallMinWorkgroups)
     return launch_router_shape<RouterShapeTall>(gw, x, T, logits, s);
+  // a workgroup of 256 x 64 tiles is bound by its own MFMA work: while those leave CUs idle,
+  // 128 x 64 tiles give twice the workgroups
+  const int64_t wide = (T + RouterShape::kWT - 1) / RouterShape::kWT *
+                       ((E + RouterShape::kRows - 1) / RouterShape::kRows);
+  if (wide < device_cus()) return launch_router_shape<RouterShape128>(gw, x, T, logits, s);
   return launch_router_shape<RouterShape>(gw, x, T, logits, s);
 }
 
