@@ -354,7 +354,7 @@ template <int TT, int MAXB>
 __device__ __forceinline__ void gate_up_group(const GroupWeights& gw, const uint16_t* __restrict__ x,
                                               int g, int n, int row0, const int32_t* toks,
                                               int slice, int nslices, int act_ld,
-                                              uint16_t* __restrict__ act) {
+                                              uint16_t* __restrict__ act, u32x4* lds) {
   const bool shared = g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int c0 = blockIdx.x * 16;
@@ -376,7 +376,6 @@ __device__ __forceinline__ void gate_up_group(const GroupWeights& gw, const uint
   const char* abase[2] = {wgt + static_cast<int64_t>(c0) * H * 2,
                           wup + static_cast<int64_t>(c0) * H * 2};
   const uint32_t aoff = static_cast<uint32_t>((q * H + 8 * r) * 2);
-  __shared__ u32x4 lds[split_lds_u4<TT>()];
   for (int p0 = 16 * TT * slice; p0 < n; p0 += 16 * TT * nslices) {
     const uint16_t* bp[TT][4];
 #pragma unroll
@@ -407,6 +406,25 @@ __device__ __forceinline__ void gate_up_group(const GroupWeights& gw, const uint
   }
 }
 
+// A launch planned for two token tiles per pass runs a group of at most 16 rows (one tile)
+// with the one-tile pass instead, so the second tile's token loads and MFMAs, all padding, are
+// not issued (Qwen3-30B-A3B T=192 213.5 -> 211.1 us, T=256 227.9 -> 226.1 us). Its k-blocks
+// still come one per chunk: two per chunk, as the one-tile plan loads them, made the whole
+// launch slower (gate_up at T=256 144 -> 153 us).
+template <int TT, int MAXB>
+__device__ __forceinline__ void gate_up_rows(const GroupWeights& gw, const uint16_t* __restrict__ x,
+                                             int g, int n, int row0, const int32_t* toks,
+                                             int slice, int nslices, int act_ld,
+                                             uint16_t* __restrict__ act, u32x4* lds) {
+  if constexpr (TT == 2) {
+    if (n <= 16 && nslices == 1) {
+      gate_up_group<1, 1>(gw, x, g, n, row0, toks, slice, nslices, act_ld, act, lds);
+      return;
+    }
+  }
+  gate_up_group<TT, MAXB>(gw, x, g, n, row0, toks, slice, nslices, act_ld, act, lds);
+}
+
 template <int TT, int MAXB>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
     GroupWeights gw, const uint16_t* __restrict__ x, const int32_t* __restrict__ counts,
@@ -417,8 +435,9 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_kernel(
   const bool shared = gs.g == gw.E;
   const int n = shared ? T : counts[gs.g];
   const int row0 = shared ? gw.sh_row0 : offsets[gs.g];
-  gate_up_group<TT, MAXB>(gw, x, gs.g, n, row0, shared ? nullptr : perm_tok + row0, gs.slice,
-                          gs.nslices, act_ld, act);
+  __shared__ u32x4 lds[split_lds_u4<TT>()];
+  gate_up_rows<TT, MAXB>(gw, x, gs.g, n, row0, shared ? nullptr : perm_tok + row0, gs.slice,
+                         gs.nslices, act_ld, act, lds);
 }
 
 // Rows of routed group g from the selected experts idx [T][k] (int32, every id in [0, E)), in
@@ -539,7 +558,8 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_perm_kernel(
   } else {
     group_rows<KMAX>(idx, T, k, gw.E, gs.g, po, n, row0, toks);
   }
-  gate_up_group<TT, MAXB>(gw, x, gs.g, n, row0, toks, gs.slice, gs.nslices, act_ld, act);
+  __shared__ u32x4 lds[split_lds_u4<TT>()];
+  gate_up_rows<TT, MAXB>(gw, x, gs.g, n, row0, toks, gs.slice, gs.nslices, act_ld, act, lds);
 }
 
 // The routing of a batch of T <= kInlineRouteTokens tokens with T*k <= kInlineRouteEntries,
@@ -674,7 +694,8 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void gate_up_bf16_routed_kerne
     n = T;
     row0 = gw.sh_row0;
   }
-  gate_up_group<1, MAXB>(gw, x, g, n, row0, toks, slice, nslices, act_ld, act);
+  __shared__ u32x4 lds[split_lds_u4<1>()];
+  gate_up_group<1, MAXB>(gw, x, g, n, row0, toks, slice, nslices, act_ld, act, lds);
 }
 
 hipError_t launch_gate_up_bf16(const GroupWeights& gw, const void* x, const int32_t* counts,
@@ -763,20 +784,13 @@ hipError_t launch_gate_up_bf16_perm(const GroupWeights& gw, const void* x, const
 // ---- down projection ---------------------------------------------------------------------
 // Workgroup (row block hb, group g): output columns [32hb, 32hb+32) of H for every token row of
 // the group: out[row, h] = bf16(act[row, :Ig] . Wd_g[h, :Ig]) (qwen3_5.py:837, :868, :917).
+// Output columns [h0, h0 + 32) of group g's n rows from row0 on (K = Ig), TT token tiles per
+// pass; the passes slice, slice + nslices, ... of the group.
 template <int TT, int MAXB>
-__global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
-    GroupWeights gw, const uint16_t* __restrict__ act, int act_ld,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T,
-    int shared_extra, int width, uint16_t* __restrict__ out) {
-  const GroupSlice gs = group_slice(gw, shared_extra, counts);
-  const int g = gs.g;
-  if (g < 0) return;
+__device__ __forceinline__ void down_group(const GroupWeights& gw, const uint16_t* __restrict__ act,
+                                           int act_ld, int g, int Ig, int n, int row0, int slice,
+                                           int nslices, uint16_t* __restrict__ out, u32x4* lds) {
   const bool shared = g == gw.E;
-  const int Ig = shared ? gw.Is : gw.I;
-  if (Ig != width) return;          // groups of another width run in their own launch
-  const int n = shared ? T : counts[g];
-  if (n == 0) return;
-  const int row0 = shared ? gw.sh_row0 : offsets[g];
   const int H = gw.H;
   const int h0 = blockIdx.x * 32;
   const int W = blockDim.x >> 6;
@@ -788,8 +802,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
   const char* abase[2] = {wd + static_cast<int64_t>(h0) * Ig * 2,
                           wd + static_cast<int64_t>(h0 + 16) * Ig * 2};
   const uint32_t aoff = static_cast<uint32_t>((q * Ig + 8 * r) * 2);
-  __shared__ u32x4 lds[split_lds_u4<TT>()];
-  for (int p0 = 16 * TT * gs.slice; p0 < n; p0 += 16 * TT * gs.nslices) {
+  for (int p0 = 16 * TT * slice; p0 < n; p0 += 16 * TT * nslices) {
     const uint16_t* bp[TT][4];
 #pragma unroll
     for (int j = 0; j < TT; ++j)
@@ -812,6 +825,34 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
     }
     __syncthreads();   // partial sums read before the next pass reuses the slots
   }
+}
+
+// Workgroup (row block hb, group g): output columns [32hb, 32hb+32) of H for every token row of
+// the group: out[row, h] = bf16(act[row, :Ig] . Wd_g[h, :Ig]) (qwen3_5.py:837, :868, :917). A
+// launch planned for two token tiles runs groups of at most 16 rows with the one-tile pass
+// (T=192 down 72.1 -> 70.3 us).
+template <int TT, int MAXB>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void down_bf16_kernel(
+    GroupWeights gw, const uint16_t* __restrict__ act, int act_ld,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, int T,
+    int shared_extra, int width, uint16_t* __restrict__ out) {
+  const GroupSlice gs = group_slice(gw, shared_extra, counts);
+  const int g = gs.g;
+  if (g < 0) return;
+  const bool shared = g == gw.E;
+  const int Ig = shared ? gw.Is : gw.I;
+  if (Ig != width) return;          // groups of another width run in their own launch
+  const int n = shared ? T : counts[g];
+  if (n == 0) return;
+  const int row0 = shared ? gw.sh_row0 : offsets[g];
+  __shared__ u32x4 lds[split_lds_u4<TT>()];
+  if constexpr (TT == 2) {
+    if (n <= 16 && gs.nslices == 1) {
+      down_group<1, 1>(gw, act, act_ld, g, Ig, n, row0, gs.slice, gs.nslices, out, lds);
+      return;
+    }
+  }
+  down_group<TT, MAXB>(gw, act, act_ld, g, Ig, n, row0, gs.slice, gs.nslices, out, lds);
 }
 
 hipError_t launch_down_bf16(const GroupWeights& gw, const void* act, int act_ld,
