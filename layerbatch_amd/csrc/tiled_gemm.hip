@@ -50,9 +50,11 @@
 namespace lbmoe {
 
 // wide: 2 x 4 waves of 128 x 64 (256 tokens), 3 weight + 2 token stages of 64-k tiles; narrow:
-// 2 x 4 waves of 128 x 32 (128 tokens), 3 stages of both
+// 4 x 2 waves of 64 x 64 (128 tokens; four fragment reads per k-step instead of the five of
+// 2 x 4 waves of 128 x 32: E=512 T=4096 gate_up 396 -> 390 us, layer 710.6 -> 707.4 us
+// median), 3 stages of both
 using Wide = TileShape<2, 4, 2, 64, 3, 2>;
-using Narrow = TileShape<2, 4, 1, 64, 3>;
+using Narrow = TileShape<4, 2, 2, 64, 3>;
 // tiny: 4 x 2 waves of 64 x 32 (64 tokens), for a group's last few rows
 using Tiny = TileShape<4, 2, 1, 64, 3>;
 // router logits: 4 x 2 waves of 64 x 32 (256 experts x 64 tokens); for at most 128 experts
