@@ -11,15 +11,18 @@
 
 namespace lbmoe {
 
-// One workgroup per token. Per group of kCombineSlots slots, the token's (row, weight) pairs
-// are read first, then every thread issues its row loads together before accumulating, so the
-// loads overlap. All loads are unconditional (indices past k or rows of dropped pairs read a
-// real entry and are masked afterwards): a load under a condition would make the compiler
-// wait for every earlier load at the join. The expert-output rows are read once and y is
-// written once, both non-temporally, so neither stream displaces cached data (Qwen3-30B-A3B
-// T=8192: 58.8 -> 50.4 us; fp8 E=512 T=16384: 168 -> 147 us).
-constexpr int kCombineSlots = 8;   // slots whose row loads are in flight together
-
+// One workgroup per token. Per group of SLOTS slots, the token's (row, weight) pairs are read
+// first, then every thread issues its row loads together before accumulating, so the loads
+// overlap; the shared expert's row goes out with the first group's. SLOTS covers k for the
+// usual widths (8 for k <= 8, 10 for k <= 10), so all of a token's rows are in flight at once:
+// with groups of 8 at k = 10 the last two slots and the shared row took two more round trips
+// (E=512 T=4096 combine 39.9 -> 36.9 us, T=128 7.4 -> 6.4 us in event-separated calls; fp8
+// T=16384, bound by its 805 MB, unchanged). All loads are unconditional (indices past k or rows of
+// dropped pairs read a real entry and are masked afterwards): a load under a condition would
+// make the compiler wait for every earlier load at the join. The expert-output rows are read
+// once and y is written once, both non-temporally, so neither stream displaces cached data
+// (Qwen3-30B-A3B T=8192: 58.8 -> 50.4 us; fp8 E=512 T=16384: 168 -> 147 us).
+template <int SLOTS, bool SHARED>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ rows,
                                                       const int32_t* __restrict__ inv,
                                                       const uint16_t* __restrict__ topw,
@@ -29,24 +32,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   const int t = blockIdx.x;
   const int32_t* inv_t = inv + static_cast<int64_t>(t) * k;
   const uint16_t* w_t = topw + static_cast<int64_t>(t) * k;
+  const uint16_t* sh_row = rows + static_cast<int64_t>(sh_row0 + t) * H;
   for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < k; s0 += kCombineSlots) {
-      int p[kCombineSlots];
-      float w[kCombineSlots];
+    u32x4 osh;
+    if constexpr (SHARED) osh = ld16_stream(sh_row + c);
+    for (int s0 = 0; s0 < k; s0 += SLOTS) {
+      int p[SLOTS];
+      float w[SLOTS];
 #pragma unroll
-      for (int i = 0; i < kCombineSlots; ++i) {
+      for (int i = 0; i < SLOTS; ++i) {
         const int s = min(s0 + i, k - 1);
         const bool in = s0 + i < k;
         p[i] = in ? inv_t[s] : -1;
         w[i] = bf2f(w_t[s]);
       }
-      u32x4 o[kCombineSlots];
+      u32x4 o[SLOTS];
 #pragma unroll
-      for (int i = 0; i < kCombineSlots; ++i)
+      for (int i = 0; i < SLOTS; ++i)
         o[i] = ld16_stream(rows + static_cast<int64_t>(max(p[i], 0)) * H + c);
 #pragma unroll
-      for (int i = 0; i < kCombineSlots; ++i) {
+      for (int i = 0; i < SLOTS; ++i) {
         const bool use = p[i] >= 0;        // dropped pairs and slots past k add nothing
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -55,13 +61,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
         }
       }
     }
-    if (sgate != nullptr) {
+    if constexpr (SHARED) {
       const float g = sgate[t];
-      const u32x4 o = ld16_stream(rows + static_cast<int64_t>(sh_row0 + t) * H + c);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc[2 * q] += g * bf_lo(o[q]);
-        acc[2 * q + 1] += g * bf_hi(o[q]);
+        acc[2 * q] += g * bf_lo(osh[q]);
+        acc[2 * q + 1] += g * bf_hi(osh[q]);
       }
     }
     u32x4 pk;
@@ -170,10 +175,20 @@ hipError_t launch_down_combine_small(const GroupWeights& gw, const void* act, in
 hipError_t launch_combine(const void* out_rows, const int32_t* inv, const void* topw,
                           const float* sgate, int64_t T, int k, int H, bool shared, void* y,
                           hipStream_t s) {
-  combine_kernel<<<static_cast<unsigned>(T), 256, 0, s>>>(
-      static_cast<const uint16_t*>(out_rows), inv, static_cast<const uint16_t*>(topw),
-      shared ? sgate : nullptr, static_cast<int>(T), k, H, static_cast<int>(T) * k,
-      static_cast<uint16_t*>(y));
+#define LBMOE_COMBINE(SLOTS, SH)                                                              \
+  combine_kernel<SLOTS, SH><<<static_cast<unsigned>(T), 256, 0, s>>>(                         \
+      static_cast<const uint16_t*>(out_rows), inv, static_cast<const uint16_t*>(topw), sgate,  \
+      static_cast<int>(T), k, H, static_cast<int>(T) * k, static_cast<uint16_t*>(y))
+  if (shared) {
+    if (k <= 8) LBMOE_COMBINE(8, true);
+    else if (k <= 10) LBMOE_COMBINE(10, true);
+    else LBMOE_COMBINE(8, true);
+  } else {
+    if (k <= 8) LBMOE_COMBINE(8, false);
+    else if (k <= 10) LBMOE_COMBINE(10, false);
+    else LBMOE_COMBINE(8, false);
+  }
+#undef LBMOE_COMBINE
   return hipGetLastError();
 }
 
