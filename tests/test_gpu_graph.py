@@ -141,11 +141,13 @@ def test_decode_bucket_graphs(gpu, shape, buckets, checked):
 # Two decoder layers' blocks (different weights) on two streams, as LayerBatch decode runs group
 # A's unit t on la_stream while group B's unit t-1 runs on fa_stream (layer_batch.py:175-212):
 # decode-sized batches (weight-streaming GEMMs, the permutation inside gate_up), prefill-sized
-# ones (LDS-tiled GEMMs with the persistent gate_up's work queues in the workspace), and the fp8
-# E=512 layer with its shared expert.
+# ones (LDS-tiled GEMMs with the persistent gate_up's work queues in the workspace), the fp8
+# E=512 layer with its shared expert, and fp8 prefill batches large enough for the persistent
+# fp8 gate_up.
 @pytest.mark.parametrize("name,Ta,Tb,fp8", [("qwen3-30b-a3b", 48, 80, False),
                                           ("qwen3-30b-a3b", 1024, 2048, False),
-                                          ("qwen3-next-e512", 128, 600, True)])
+                                          ("qwen3-next-e512", 128, 600, True),
+                                          ("qwen3-30b-a3b", 8192, 6000, True)])
 def test_two_streams_overlapping_calls(gpu, name, Ta, Tb, fp8):
     """Calls on two streams with one workspace each and no synchronisation between the
     streams give, bit for bit, the outputs of the same calls made one after another."""
