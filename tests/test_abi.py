@@ -278,3 +278,23 @@ def test_stale_tiled_copies_are_dropped():
             assert not moe._tiled_current(ex, src, "experts weights")
         assert ex.gate_up_tiled is None and ex.down_tiled is None
         assert not moe._tiled_current(ex, src, "experts weights")   # dropped: no second warning
+
+
+@pytest.mark.parametrize("kw,fp8,max_T", [
+    ({}, False, 1348),                                                     # Qwen3-30B-A3B
+    (dict(hidden_size=2048, num_experts=512, top_k=10, moe_intermediate_size=512,
+          shared_intermediate_size=512), False, 1075),                    # E=512 + shared
+    (dict(hidden_size=2048, num_experts=512, top_k=10, moe_intermediate_size=512,
+          shared_intermediate_size=512), True, 953),                      # the same in fp8
+])
+def test_static_workspace_capacity(lbmoe, kw, fp8, max_T):
+    """The largest batches lbmoe_forward_static takes (the figures the integration guide
+    quotes): max_T tokens fit in LBMOE_STATIC_WORKSPACE_BYTES, max_T + 1 do not."""
+    L = _layer(**kw)
+    if fp8:
+        L.weight_dtype = _lib.LBMOE_W_FP8_E4M3
+    n = ctypes.c_size_t(0)
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), max_T, ctypes.byref(n)) == OK
+    assert n.value <= _lib.LBMOE_STATIC_WORKSPACE_BYTES
+    assert lbmoe.lbmoe_workspace_size(ctypes.byref(L), max_T + 1, ctypes.byref(n)) == OK
+    assert n.value > _lib.LBMOE_STATIC_WORKSPACE_BYTES
