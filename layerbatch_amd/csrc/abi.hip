@@ -434,12 +434,14 @@ static int32_t forward_impl(const lbmoe_layer* layer, const void* x, int64_t T, 
   float* sgate = sh ? at<float>(ws, w, R_SGATE) : nullptr;
   LBMOE_TRY(ev->mark(s));
   if (!norm && route_in_router(L, T, sh)) {
-    // logits, selection and the permutation's count pass in one launch (profiled calls time it
-    // as the router stage, the routing stage then being empty)
+    // logits, selection and the permutation's count pass in one launch, or two with the k range
+    // split (profiled calls time it as the router stage, the routing stage then being empty);
+    // the split's partial sums go to the expert-output region, which only the down GEMM writes
     LBMOE_TRY(launch_router_route(x, L.gate_weight, L.logit_bias, L.shared_expert_gate, T,
                                   L.num_experts, L.hidden_size, L.top_k, logits,
                                   static_cast<int32_t*>(idx), topw, sgate,
-                                  at<int32_t>(ws, w, R_HIST), at<int32_t>(ws, w, R_LRANK), s));
+                                  at<int32_t>(ws, w, R_HIST), at<int32_t>(ws, w, R_LRANK),
+                                  at<void>(ws, w, R_OUT), w.bytes[R_OUT], s));
     LBMOE_TRY(ev->mark(s));
     LBMOE_TRY(ev->mark(s));
     return run_experts(L, x, idx, 4, topw, sgate, T, y, ws, w, sh, s, ev, false, nullptr, true,

@@ -262,10 +262,12 @@ bool router_is_tiled(int64_t T, int E, int H);
 // the tile list (launch_scatter_build).
 bool router_route_supported(int E, int H, int k);
 int64_t router_route_chunks(int64_t T, int k);
+// part: scratch for the k-split partial sums (part_bytes of it; with too little the router runs
+// as one launch)
 hipError_t launch_router_route(const void* x, const void* wg, const float* bias, const void* w_sg,
                                int64_t T, int E, int H, int k, void* logits, int32_t* idx,
                                void* topw, float* sgate, int32_t* hist, int32_t* lrank,
-                               hipStream_t s);
+                               void* part, size_t part_bytes, hipStream_t s);
 hipError_t launch_perm_scan(const int32_t* hist, int nchunks, int E, int32_t* base,
                             int32_t* totals, hipStream_t s);
 // The chunked permutation of launch_permute as two steps, for the prefill GEMMs: the count

@@ -378,12 +378,81 @@ enum TileMode { kDown = 0, kGateUp = 1, kRouter = 2 };
 // same workgroup.
 template <class S>
 constexpr int kStagedLogitStride = S::kRows + 8;   // uint16 entries; + 8 against bank conflicts
-template <int MODE, class S, int kLdsCap = kLdsU4, bool PERSIST = false, bool STAGE = false>
+
+// The router tile's accumulators (wave (wm, wn) of shape S) rounded to bf16 into LDS as rows of
+// kStagedLogitStride entries per token, then the rows of its ne = min(S::kRows, E - c0) experts
+// stored to dst (local token tl of the n - r0 left at row row0 + r0 + tl, dst_ld per row) with
+// 16-byte lanes. Called by every thread of the workgroup once no wave reads lds any more.
+template <class S>
+__device__ __forceinline__ void stage_logits(const f32x16 (&acc)[S::kMT][S::kNT], int E, int n,
+                                             int r0, int row0, int c0, uint16_t* __restrict__ dst,
+                                             int dst_ld, u32x4* __restrict__ lds) {
+  constexpr int kStride = kStagedLogitStride<S>, kMT = S::kMT, kNT = S::kNT, kRW = S::kRW;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = w % S::kWavesM, wn = w / S::kWavesM;
+  const int col = lane & 31, rq = 4 * (lane >> 5);
+  ring_barrier();                                           // every wave is done with the ring
+  uint16_t* sl = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) {
+    const int tl = wn * (kNT * 32) + 32 * t + col;          // token within the tile
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int e = wm * kRW + 32 * i + 8 * v4 + rq;     // expert within the tile
+        *reinterpret_cast<u32x2*>(sl + tl * kStride + e) =
+            u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
+                  pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
+      }
+  }
+  ring_barrier();
+  const int ntok = min(S::kWT, n - r0), ne = min(S::kRows, E - c0);
+  if ((ne & 7) == 0 && (dst_ld & 7) == 0 && (c0 & 7) == 0) {
+    const int cpr = ne / 8;                                 // 16-byte chunks per row
+    for (int i = threadIdx.x; i < ntok * cpr; i += kThreads) {
+      const int tl = i / cpr, c = i - tl * cpr;
+      *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + 8 * c) =
+          *reinterpret_cast<const u32x4*>(sl + tl * kStride + 8 * c);
+    }
+  } else {
+    for (int i = threadIdx.x; i < ntok * ne; i += kThreads) {
+      const int tl = i / ne, e = i - tl * ne;
+      dst[static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + e] = sl[tl * kStride + e];
+    }
+  }
+}
+
+// Partial sums of a router tile over a k range, in fp32: accumulator element 4 q + v of tile
+// (i, t) of wave w, lane l lands at float (((((i * kNT + t) * 4 + q) * kWaves + w) * 64 + l) * 4
+// + v, so every store and load instruction moves 1 KB of consecutive bytes.
+template <class S>
+constexpr int kPartialFloats = S::kMT * S::kNT * 16 * kThreads;
+template <class S>
+__device__ __forceinline__ void store_partial(const f32x16 (&acc)[S::kMT][S::kNT],
+                                              float* __restrict__ part) {
+  f32x4* p = reinterpret_cast<f32x4*>(part) + threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < S::kMT; ++i)
+#pragma unroll
+    for (int t = 0; t < S::kNT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        p[((i * S::kNT + t) * 4 + q) * kThreads] =
+            f32x4{acc[i][t][4 * q], acc[i][t][4 * q + 1], acc[i][t][4 * q + 2], acc[i][t][4 * q + 3]};
+}
+// PARTIAL (router only): only k-tiles kt0 .. kt0 + nkt - 1 of the product, whose fp32 sums go
+// to part (store_partial) instead of logits.
+template <int MODE, class S, int kLdsCap = kLdsU4, bool PERSIST = false, bool STAGE = false,
+          bool PARTIAL = false>
 __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint16_t* __restrict__ src,
                                              int src_ld, const int32_t* __restrict__ perm_tok,
                                              int g, int r0, int n, int row0, int wt,
                                              uint16_t* __restrict__ dst, int dst_ld,
-                                             u32x4* __restrict__ lds, WorkQueue* wq = nullptr) {
+                                             u32x4* __restrict__ lds, WorkQueue* wq = nullptr,
+                                             int kt0 = 0, int nkt = 0,
+                                             float* __restrict__ part = nullptr) {
   constexpr bool GATEUP = MODE == kGateUp, ROUTER = MODE == kRouter;
   constexpr int kMT = S::kMT, kNT = S::kNT, kRW = S::kRW, kWavesM = S::kWavesM;
   constexpr int kBK = S::kBK, kStages = S::kStages, kChunks = S::kChunks;
@@ -393,6 +462,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   constexpr int kRows = S::kRows;                  // weight rows of the tile
   static_assert(ROUTER || kRows == kWM, "expert GEMMs take kWM weight rows per tile");
   static_assert(!GATEUP || kMT % 2 == 0, "gate_up pairs a wave's gate tiles with its up tiles");
+  static_assert(!PARTIAL || (ROUTER && !STAGE), "partial sums are router tiles");
   const bool shared = !ROUTER && g == gw.E;
   const int Ig = shared ? gw.Is : gw.I;
   const int H = gw.H;
@@ -458,6 +528,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     }
     ars[i] = raw_rsrc(base);
     aoff[i] = static_cast<uint32_t>((static_cast<int64_t>(grow) * K + 8 * j) * 2);
+    if constexpr (PARTIAL) aoff[i] += static_cast<uint32_t>(kt0 * kBK * 2);
   }
   // Weight bytes between k-tile kt and kt + 1 of a copy: kBK elements along the checkpoint
   // rows, or one whole k-tile block in the tiled layout (pack_tiled_kernel), where the kWM x
@@ -488,6 +559,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     const int p = min(r0 + lt, n - 1);   // rows past the group repeat a valid row; not stored
     const int srow = ROUTER ? p : (GATEUP ? (shared ? p : perm_tok[row0 + p]) : row0 + p);
     boff[i] = static_cast<uint32_t>((static_cast<int64_t>(srow) * src_ld + 8 * j) * 2);
+    if constexpr (PARTIAL) boff[i] += static_cast<uint32_t>(kt0 * kBK * 2);
   }
 
   f32x16 acc[kMT][kNT];
@@ -534,7 +606,7 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
   // stage kt+1's first fragments and refills stage kt's buffer with k-tile kt+kStages, all
   // interleaved with the last k-step's MFMAs, so neither the copy issue nor the LDS read
   // latency of the next k-tile stands between two MFMAs.
-  const int nk = K / kBK;
+  const int nk = PARTIAL ? nkt : K / kBK;
   // Wide expert tiles (MFMA-bound) put only stage 0 out before the first wait. A wave reaches
   // its wait once it has issued every copy before it, and the CU's copy path takes the waves'
   // copies in turn: with the whole ring issued up front, the second wave of each SIMD saw its
@@ -752,40 +824,12 @@ __device__ __forceinline__ void tile_product(const GroupWeights& gw, const uint1
     }
     ring_barrier();
     store_staged<kCols, S::kWT, !GATEUP>(lds, dst, dst_ld, row0, r0, n, c0);   // down: read once
+  } else if constexpr (PARTIAL) {
+    store_partial<S>(acc, part);
   } else if constexpr (STAGE) {
     // logits through LDS: staged rows, then whole rows stored with 16-byte lanes
-    constexpr int kStride = kStagedLogitStride<S>;
-    static_assert(S::kWT * kStride * 2 <= kLdsCap * 16, "staged logits exceed the ring");
-    ring_barrier();                                           // every wave is done with the ring
-    uint16_t* sl = reinterpret_cast<uint16_t*>(lds);
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int tl = wn * (kNT * 32) + 32 * t + col;          // token within the tile
-#pragma unroll
-      for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) {
-          const int e = wm * kRW + 32 * i + 8 * v4 + rq;     // expert within the tile
-          *reinterpret_cast<u32x2*>(sl + tl * kStride + e) =
-              u32x2{pack_bf2(acc[i][t][4 * v4], acc[i][t][4 * v4 + 1]),
-                    pack_bf2(acc[i][t][4 * v4 + 2], acc[i][t][4 * v4 + 3])};
-        }
-    }
-    ring_barrier();
-    const int E = gw.E, ntok = min(S::kWT, n - r0), ne = min(kRows, E - c0);
-    if ((ne & 7) == 0 && (dst_ld & 7) == 0 && (c0 & 7) == 0) {
-      const int cpr = ne / 8;                                 // 16-byte chunks per row
-      for (int i = threadIdx.x; i < ntok * cpr; i += kThreads) {
-        const int tl = i / cpr, c = i - tl * cpr;
-        *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + 8 * c) =
-            *reinterpret_cast<const u32x4*>(sl + tl * kStride + 8 * c);
-      }
-    } else {
-      for (int i = threadIdx.x; i < ntok * ne; i += kThreads) {
-        const int tl = i / ne, e = i - tl * ne;
-        dst[static_cast<int64_t>(row0 + r0 + tl) * dst_ld + c0 + e] = sl[tl * kStride + e];
-      }
-    }
+    static_assert(S::kWT * kStagedLogitStride<S> * 2 <= kLdsCap * 16, "staged logits exceed the ring");
+    stage_logits<S>(acc, gw.E, n, r0, row0, c0, dst, dst_ld, lds);
   } else {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
@@ -827,42 +871,35 @@ void router_tiled_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
                                                      wt, logits, gw.E, lds);
 }
 
-// Router logits, selection and the first permutation pass in one workgroup per 64-token block
-// b (E <= 128, so one tile holds every expert): the tile's logits stay in LDS (STAGE), and each
-// wave selects 8 tokens at once from them (route_select8, an 8-lane group per token, experts
-// 8j + u on lane u of the group) and keeps their ids in LDS; then, for each slot s, a wave ranks
-// the block's 64 entries of chunk c = s * nb + b among equal experts (ballot match, in token
-// order) into lrank and writes the chunk's per-expert counts to hist[e * k * nb + c].
-// perm_expert_scan and scatter_build_kernel finish the sort. Saves the route and count
-// launches and the logits' round trip. EPG: experts per lane, ceil(E / 8) rounded up to 8 or 16.
 constexpr int kRouteMaxK = 16;
+// LDS of the selection: the staged logits of a 64-token block, then the ids and per-wave counts.
+constexpr int kRouteStagedBytes = RouterShape128::kWT * kStagedLogitStride<RouterShape128> * 2;
+constexpr int kRouteLdsBytes =
+    kRouteStagedBytes + (RouterShape128::kWT * kRouteMaxK + kWaves * RouterShape128::kRows) * 4;
+static_assert(kRouteStagedBytes % 16 == 0 && kRouteLdsBytes % 16 == 0, "16-byte LDS units");
+
+// Selection and the first permutation pass of 64-token block b (E <= 128) from its logits,
+// staged in lds by stage_logits: each wave selects 8 tokens at once (route_select8, an 8-lane
+// group per token, experts 8j + u on lane u of the group) and keeps their ids in LDS; then, for
+// each slot s, a wave ranks the block's 64 entries of chunk c = s * nb + b among equal experts
+// (ballot match, in token order) into lrank and writes the chunk's per-expert counts to
+// hist[e * k * nb + c]. perm_expert_scan and scatter_build_kernel finish the sort. EPG: experts
+// per lane, ceil(E / 8) rounded up to 8 or 16.
 template <int EPG>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
-void router_route_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
-                         const float* __restrict__ bias, const uint16_t* __restrict__ w_sg, int k,
-                         int nbits, int nb, uint16_t* __restrict__ logits, int32_t* __restrict__ idx,
-                         uint16_t* __restrict__ topw, float* __restrict__ sgate,
-                         int32_t* __restrict__ hist, int32_t* __restrict__ lrank) {
+__device__ __forceinline__ void route_block(const uint16_t* __restrict__ x, int T, int E, int H,
+                                            const float* __restrict__ bias,
+                                            const uint16_t* __restrict__ w_sg, int k, int nbits,
+                                            int nb, int b, int32_t* __restrict__ idx,
+                                            uint16_t* __restrict__ topw, float* __restrict__ sgate,
+                                            int32_t* __restrict__ hist,
+                                            int32_t* __restrict__ lrank, u32x4* lds) {
   using S = RouterShape128;
   constexpr int kStride = kStagedLogitStride<S>, kPerWave = S::kWT / kWaves;
   static_assert(kPerWave == kWave / 8, "a wave selects one token per 8-lane group");
   static_assert(8 * EPG <= S::kRows, "experts per lane exceed the tile");
-  // The ring is the kernel's only LDS object: the ids and counts live in it, behind the staged
-  // logits. With a second __shared__ array in the kernel the compiler made every LDS read of
-  // the k-loop wait for all global->LDS copies in flight (s_waitcnt vmcnt(0)), which drained
-  // the ring each k-tile (the tile took 30 instead of 19 us at Qwen3-30B-A3B T=8192).
-  __shared__ u32x4 lds[S::kRingU4];
-  constexpr int kStagedBytes = S::kWT * kStride * 2;
-  static_assert(kStagedBytes % 16 == 0 &&
-                    kStagedBytes + (S::kWT * kRouteMaxK + kWaves * S::kRows) * 4 <= S::kRingU4 * 16,
-                "ids and counts exceed the ring");
-  int32_t* s_idx = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(lds) + kStagedBytes);
+  int32_t* s_idx = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(lds) + kRouteStagedBytes);
   int32_t* s_cnt = s_idx + S::kWT * kRouteMaxK;              // [kWaves][S::kRows]
-  const int b = xcd_item(blockIdx.x, nb);
-  if (b < 0) return;
-  const int E = gw.E, H = gw.H, t0 = b * S::kWT, nt = min(S::kWT, T - t0);
-  tile_product<kRouter, S, S::kRingU4, false, true>(gw, x, H, nullptr, 0, t0, T, 0, 0, logits, E,
-                                                    lds);
+  const int t0 = b * S::kWT, nt = min(S::kWT, T - t0);
   const uint16_t* sl = reinterpret_cast<const uint16_t*>(lds);
   const int lane = lane_id(), u = lane & 7;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -905,6 +942,87 @@ void router_route_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
   }
 }
 
+// Router logits, selection and the first permutation pass in one workgroup per 64-token block
+// b (E <= 128, so one tile holds every expert): the tile's logits stay in LDS (STAGE) for
+// route_block. Saves the route and count launches and the logits' round trip.
+template <int EPG>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
+void router_route_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
+                         const float* __restrict__ bias, const uint16_t* __restrict__ w_sg, int k,
+                         int nbits, int nb, uint16_t* __restrict__ logits, int32_t* __restrict__ idx,
+                         uint16_t* __restrict__ topw, float* __restrict__ sgate,
+                         int32_t* __restrict__ hist, int32_t* __restrict__ lrank) {
+  using S = RouterShape128;
+  // The ring is the kernel's only LDS object: the ids and counts live in it, behind the staged
+  // logits. With a second __shared__ array in the kernel the compiler made every LDS read of
+  // the k-loop wait for all global->LDS copies in flight (s_waitcnt vmcnt(0)), which drained
+  // the ring each k-tile (the tile took 30 instead of 19 us at Qwen3-30B-A3B T=8192).
+  __shared__ u32x4 lds[S::kRingU4];
+  static_assert(kRouteLdsBytes <= S::kRingU4 * 16, "ids and counts exceed the ring");
+  const int b = xcd_item(blockIdx.x, nb);
+  if (b < 0) return;
+  tile_product<kRouter, S, S::kRingU4, false, true>(gw, x, gw.H, nullptr, 0, b * S::kWT, T, 0, 0,
+                                                    logits, gw.E, lds);
+  route_block<EPG>(x, T, gw.E, gw.H, bias, w_sg, k, nbits, nb, b, idx, topw, sgate, hist, lrank,
+                   lds);
+}
+
+// The same work in two launches where the blocks alone would leave CUs idle (small and mid-size
+// batches): the tile's per-workgroup time is set by the bytes it streams (the whole router
+// weight, 512 KB at E = 128, H = 2048, plus its tokens' rows), whatever the batch, so the k
+// range is split. router_partial_kernel: workgroup (b, p) forms block b's fp32 sums over
+// k-tiles [p nkt, (p + 1) nkt) into part + (b * splits + p) * kPartialFloats.
+// router_select_kernel: block b's workgroup adds its splits' sums in p order (a fixed order,
+// so the logits do not depend on timing), rounds them to bf16 and runs route_block.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 4)))
+void router_partial_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T, int nb,
+                           int splits, float* __restrict__ part) {
+  using S = RouterShape128;
+  __shared__ u32x4 lds[S::kRingU4];
+  const int item = xcd_item(blockIdx.x, nb * splits);
+  if (item < 0) return;
+  const int b = item / splits, p = item - b * splits;
+  const int nkt = gw.H / S::kBK / splits;
+  tile_product<kRouter, S, S::kRingU4, false, false, true>(
+      gw, x, gw.H, nullptr, 0, b * S::kWT, T, 0, 0, nullptr, 0, lds, nullptr, p * nkt, nkt,
+      part + static_cast<int64_t>(item) * kPartialFloats<S>);
+}
+
+template <int EPG, int SPLITS>
+__global__ __launch_bounds__(kThreads)
+void router_select_kernel(GroupWeights gw, const uint16_t* __restrict__ x, int T,
+                          const float* __restrict__ part, const float* __restrict__ bias,
+                          const uint16_t* __restrict__ w_sg, int k, int nbits, int nb,
+                          uint16_t* __restrict__ logits, int32_t* __restrict__ idx,
+                          uint16_t* __restrict__ topw, float* __restrict__ sgate,
+                          int32_t* __restrict__ hist, int32_t* __restrict__ lrank) {
+  using S = RouterShape128;
+  static_assert(S::kMT == 1 && S::kNT == 1, "one accumulator tile per wave");
+  __shared__ u32x4 lds[kRouteLdsBytes / 16];
+  const int b = xcd_item(blockIdx.x, nb);
+  if (b < 0) return;
+  // every split's four 16-byte pieces in flight at once, then the sums in split order
+  const f32x4* pp = reinterpret_cast<const f32x4*>(part) +
+                    static_cast<int64_t>(b) * SPLITS * (kPartialFloats<S> / 4) + threadIdx.x;
+  f32x4 v[SPLITS][4];
+#pragma unroll
+  for (int p = 0; p < SPLITS; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[p][q] = pp[(p * 4 + q) * kThreads];
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f32x4 a = v[0][q];
+#pragma unroll
+    for (int p = 1; p < SPLITS; ++p) a += v[p][q];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[0][0][4 * q + j] = a[j];
+  }
+  stage_logits<S>(acc, gw.E, T, b * S::kWT, 0, 0, logits, gw.E, lds);
+  route_block<EPG>(x, T, gw.E, gw.H, bias, w_sg, k, nbits, nb, b, idx, topw, sgate, hist, lrank,
+                   lds);
+}
+
 // explicit instantiations: with only the two launches in launch_router_route, the host pass left
 // the second one's launch stub undefined in the library
 template __global__ void router_route_kernel<8>(GroupWeights, const uint16_t*, int, const float*,
@@ -913,6 +1031,15 @@ template __global__ void router_route_kernel<8>(GroupWeights, const uint16_t*, i
 template __global__ void router_route_kernel<16>(GroupWeights, const uint16_t*, int, const float*,
                                                 const uint16_t*, int, int, int, uint16_t*,
                                                 int32_t*, uint16_t*, float*, int32_t*, int32_t*);
+#define LBMOE_SELECT_INST(EPG, SPLITS)                                                          \
+  template __global__ void router_select_kernel<EPG, SPLITS>(                                  \
+      GroupWeights, const uint16_t*, int, const float*, const float*, const uint16_t*, int, int, \
+      int, uint16_t*, int32_t*, uint16_t*, float*, int32_t*, int32_t*);
+LBMOE_SELECT_INST(8, 2)
+LBMOE_SELECT_INST(8, 4)
+LBMOE_SELECT_INST(16, 2)
+LBMOE_SELECT_INST(16, 4)
+#undef LBMOE_SELECT_INST
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -1160,10 +1287,30 @@ static int bits_of(int E) {
   return n;
 }
 
+// Splits of the router's k range (router_partial_kernel): doubled while the blocks' workgroups
+// leave CUs idle, each split keeping at least kSplitMinKTiles k-tiles, and the partial sums
+// fitting part_bytes. 1: the one-launch router_route_kernel. The selection workgroup reads
+// splits x 32 KB of sums, so more splits move bytes from the first launch's workgroups to the
+// second's: Qwen3-30B-A3B router stage at T=1024 20.3 (one launch) / 16.3 (4 splits) / 19.0 us
+// (8 splits), T=2048 24.2 / 18.8 / 21.8 us; at T=4096 4 splits 19.9 against 2 splits 21.7 us.
+constexpr int kRouteMaxSplits = 4;
+constexpr int kSplitMinKTiles = 4;
+static int router_route_splits(int64_t T, int H, size_t part_bytes) {
+  using S = RouterShape128;
+  const int64_t nb = (T + S::kWT - 1) / S::kWT;
+  const int nkt = H / S::kBK;
+  int splits = 1;
+  while (splits < kRouteMaxSplits && nb * splits < device_cus() && nkt % (2 * splits) == 0 &&
+         nkt / (2 * splits) >= kSplitMinKTiles &&
+         static_cast<size_t>(nb * 2 * splits) * kPartialFloats<S> * 4 <= part_bytes)
+    splits *= 2;
+  return splits;
+}
+
 hipError_t launch_router_route(const void* x, const void* wg, const float* bias, const void* w_sg,
                                int64_t T, int E, int H, int k, void* logits, int32_t* idx,
                                void* topw, float* sgate, int32_t* hist, int32_t* lrank,
-                               hipStream_t s) {
+                               void* part, size_t part_bytes, hipStream_t s) {
   GroupWeights gw{};
   gw.gate_up = wg;
   gw.E = E;
@@ -1173,14 +1320,35 @@ hipError_t launch_router_route(const void* x, const void* wg, const float* bias,
   const auto* ws = static_cast<const uint16_t*>(w_sg);
   auto* lg = static_cast<uint16_t*>(logits);
   auto* tw = static_cast<uint16_t*>(topw);
-  if (E <= 64)
-    router_route_kernel<8><<<round8(nb), kThreads, 0, s>>>(gw, xx, static_cast<int>(T), bias, ws, k,
-                                                           bits_of(E), nb, lg, idx, tw, sgate,
-                                                           hist, lrank);
-  else
-    router_route_kernel<16><<<round8(nb), kThreads, 0, s>>>(gw, xx, static_cast<int>(T), bias, ws,
-                                                            k, bits_of(E), nb, lg, idx, tw, sgate,
-                                                            hist, lrank);
+  const int Ti = static_cast<int>(T), nbits = bits_of(E);
+  const int splits = router_route_splits(T, H, part_bytes);
+  if (splits == 1) {
+    if (E <= 64)
+      router_route_kernel<8><<<round8(nb), kThreads, 0, s>>>(gw, xx, Ti, bias, ws, k, nbits, nb, lg,
+                                                             idx, tw, sgate, hist, lrank);
+    else
+      router_route_kernel<16><<<round8(nb), kThreads, 0, s>>>(gw, xx, Ti, bias, ws, k, nbits, nb,
+                                                              lg, idx, tw, sgate, hist, lrank);
+    return hipGetLastError();
+  }
+  auto* pt = static_cast<float*>(part);
+  router_partial_kernel<<<round8(static_cast<int64_t>(nb) * splits), kThreads, 0, s>>>(
+      gw, xx, Ti, nb, splits, pt);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+#define LBMOE_SELECT(EPG, SPLITS)                                                               \
+  router_select_kernel<EPG, SPLITS><<<round8(nb), kThreads, 0, s>>>(gw, xx, Ti, pt, bias, ws, k, \
+                                                                    nbits, nb, lg, idx, tw,     \
+                                                                    sgate, hist, lrank)
+  static_assert(kRouteMaxSplits == 4, "a selection kernel per split count");
+  if (E <= 64) {
+    if (splits == 2) LBMOE_SELECT(8, 2);
+    else LBMOE_SELECT(8, 4);
+  } else {
+    if (splits == 2) LBMOE_SELECT(16, 2);
+    else LBMOE_SELECT(16, 4);
+  }
+#undef LBMOE_SELECT
   return hipGetLastError();
 }
 

@@ -164,11 +164,15 @@ def test_block_prefill_persistent_gate_up(gpu):
 # Batches that select experts inside the tiled router (E <= 128, T >= 1024, tiled GEMMs):
 # 16 experts per lane (E = 128) under a Zipf bias, an expert count that is no multiple of 8
 # with a ragged last 64-token block, k > 8 (a lane's second slot), and a shared expert whose
-# gate the same kernel computes.
+# gate the same kernel computes. Below 256 blocks of 64 tokens the router's k range is split
+# over 2 (H = 512) or 4 (H >= 1024) workgroups whose fp32 sums the selection kernel adds: the
+# H = 2048 cases take 4 splits with 8 (E = 64) and 16 (E = 128) experts per lane.
 @pytest.mark.parametrize("shape,T,zipf", [(MoEShape(1024, 128, 8, 256, 0), 2048, True),
                                           (MoEShape(512, 100, 6, 256, 0), 1100, False),
                                           (MoEShape(512, 96, 12, 256, 0), 1024, False),
-                                          (MoEShape(512, 80, 10, 256, 384), 1200, True)])
+                                          (MoEShape(512, 80, 10, 256, 384), 1200, True),
+                                          (MoEShape(2048, 64, 6, 256, 0), 1500, False),
+                                          (MoEShape(2048, 128, 8, 256, 256), 3000, True)])
 def test_block_prefill_route_in_router(gpu, shape, T, zipf):
     bias = None
     if zipf:
