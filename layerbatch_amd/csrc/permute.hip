@@ -105,6 +105,61 @@ __global__ __launch_bounds__(64) void perm_expert_scan(const int32_t* __restrict
   if (lane == 63) totals[e] = incl;
 }
 
+// The same with the expert's counts held in registers: 256 threads, thread t taking chunks
+// t * PER .. t * PER + PER - 1 (all loads in flight at once, read once), then a block scan.
+// The one-wave form above walks up to nblk / 64 chunks per lane twice, load after load.
+template <int PER>
+__global__ __launch_bounds__(256) void perm_expert_scan_reg(const int32_t* __restrict__ hist,
+                                                            int nblk, int32_t* __restrict__ base,
+                                                            int32_t* __restrict__ totals) {
+  __shared__ int wsum[4];
+  const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int32_t* h = hist + static_cast<int64_t>(e) * nblk;
+  const int b0 = tid * PER;
+  int v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = h[min(b0 + i, nblk - 1)];   // unconditional loads
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (b0 + i >= nblk) v[i] = 0;
+    local += v[i];
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int c = wsum[w];
+    before += w < wv ? c : 0;
+    total += c;
+  }
+  int run = before + incl - local;
+  int32_t* bs = base + static_cast<int64_t>(e) * nblk;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (b0 + i < nblk) bs[b0 + i] = run;
+    run += v[i];
+  }
+  if (tid == 0) totals[e] = total;
+}
+
+// Per-expert exclusive scans of E x nblk chunk counts (hist) into base and totals.
+static void launch_expert_scan(const int32_t* hist, int nblk, int E, int32_t* base,
+                               int32_t* totals, hipStream_t s) {
+  if (nblk <= 256) perm_expert_scan_reg<1><<<E, 256, 0, s>>>(hist, nblk, base, totals);
+  else if (nblk <= 512) perm_expert_scan_reg<2><<<E, 256, 0, s>>>(hist, nblk, base, totals);
+  else if (nblk <= 1024) perm_expert_scan_reg<4><<<E, 256, 0, s>>>(hist, nblk, base, totals);
+  else if (nblk <= 2048) perm_expert_scan_reg<8><<<E, 256, 0, s>>>(hist, nblk, base, totals);
+  else perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, totals);
+}
+
 // Each workgroup first scans the E expert totals itself (exclusive, into LDS), so no separate
 // offsets pass runs between the per-expert scan and the scatter; workgroup 0 also stores the
 // offsets (E + 1 entries) for the later stages.
@@ -322,7 +377,7 @@ static hipError_t launch_permute_t(const void* idx, int64_t T, int k, int E, int
   const int nblk = static_cast<int>(perm_blocks(V));
   perm_count<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist,
                                      lrank);
-  perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
+  launch_expert_scan(hist, nblk, E, base, counts, s);
   perm_scatter<IB><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, V, nblk, base, counts,
                                        offsets, lrank, perm_tok, perm_slot, inv);
   return hipGetLastError();
@@ -341,13 +396,13 @@ hipError_t launch_perm_count_scan(const void* idx, int idx_bytes, int64_t T, int
     perm_count<8><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist, lrank);
   else
     perm_count<4><<<nblk, 64, 0, s>>>(idx, static_cast<int>(T), k, E, nbits, V, nblk, hist, lrank);
-  perm_expert_scan<<<E, 64, 0, s>>>(hist, nblk, base, counts);
+  launch_expert_scan(hist, nblk, E, base, counts, s);
   return hipGetLastError();
 }
 
 hipError_t launch_perm_scan(const int32_t* hist, int nchunks, int E, int32_t* base,
                             int32_t* totals, hipStream_t s) {
-  perm_expert_scan<<<E, 64, 0, s>>>(hist, nchunks, base, totals);
+  launch_expert_scan(hist, nchunks, E, base, totals, s);
   return hipGetLastError();
 }
 
