@@ -18,7 +18,8 @@ def check_logits(gpu_bits, x, wg, max_frac=2e-3, acc_tol=2e-5):
     The GPU accumulates in fp32 in its own order, so its value is bf16(e + d) for the exact
     dot product e and an accumulation error |d| <= acc_tol * sum_i |x_i w_i|. Every GPU logit
     must lie in [bf16(e - tol), bf16(e + tol)], and at most max_frac of them may differ from
-    the correctly rounded bf16(e) at all.
+    the correctly rounded bf16(e) at all (at least 2, so that one or two rounding-boundary
+    logits of a small batch, e.g. one token's 96 logits, do not fail the fraction).
     """
     x64 = np.asarray(x, np.float64)
     w64 = np.asarray(wg, np.float64)
@@ -28,7 +29,8 @@ def check_logits(gpu_bits, x, wg, max_frac=2e-3, acc_tol=2e-5):
     gpu_bits = np.asarray(gpu_bits, np.uint16)
     diff = gpu_bits != ref_bits
     frac = float(diff.mean()) if diff.size else 0.0
-    assert frac <= max_frac, f"{frac:.2e} of logits differ from the oracle"
+    assert int(diff.sum()) <= max(max_frac * diff.size, 2), (
+        f"{frac:.2e} of logits differ from the oracle")
     if diff.any():
         g = bf16_from_bits(gpu_bits[diff]).astype(np.float64)
         lo = bf16_round((exact[diff] - tol[diff]).astype(np.float32)).astype(np.float64)
